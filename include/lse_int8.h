@@ -1,0 +1,128 @@
+/*
+ * lse_int8.h — C ABI of the MI355X (gfx950) int8 quantized Linear forward.
+ *
+ * The reference engine routes every Llama projection through `nn.Linear.forward`, i.e.
+ * `F.linear(x, W)` with bias=False (torch/nn/modules/linear.py:130-134), from these call
+ * sites: q/k/v in `ModelRunner._project_qkv` (src/llm_serving_engine/model/model_runner.py:322-324),
+ * o_proj in `attention_output` (model_runner.py:369) and `contiguous_attention`
+ * (model_runner.py:418), gate/up/down in `LlamaMLP.forward` reached from `decoder_hidden`
+ * (model_runner.py:223). Its int8 switch (`ModelConfig.quantize`, src/llm_serving_engine/config.py:32)
+ * stops at `raise NotImplementedError("int8 weight-only quantization")` (model_runner.py:45-46).
+ * The entry points below are what a binding for that switch calls.
+ *
+ * Conventions shared by every entry point:
+ *  - All pointers are device pointers. The caller owns every buffer; the library keeps no state
+ *    beyond its compiled kernels and allocates nothing.
+ *  - Matrices are row-major. `ld*` is the row stride in elements. bf16 data travels as
+ *    `void*` (2 bytes per element, IEEE bfloat16 bit patterns).
+ *  - `stream` is a `hipStream_t` passed as `void*`. Work is enqueued on it and never
+ *    synchronised, so every entry point is safe under HIP graph capture. The null stream is
+ *    accepted but callers that capture must pass their capture stream.
+ *  - Return value: LSE_OK (0) on success; a negative LSE_E_* code for a rejected argument
+ *    (nothing was launched); a positive hipError_t from the launch otherwise.
+ *  - Results are deterministic: no atomics, and the reduction order of every output element
+ *    depends only on K (not on M, N, or the other rows), so row m of y is bit-identical whether
+ *    it is computed alone or inside a padded batch of any size up to the same kernel family.
+ */
+#ifndef LSE_INT8_H
+#define LSE_INT8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum lse_status {
+  LSE_OK = 0,
+  LSE_E_NULL = -1,        /* a required pointer is NULL (with a non-empty shape) */
+  LSE_E_SHAPE = -2,       /* negative size, or a stride smaller than the row it holds */
+  LSE_E_ALIGN = -3,       /* K, a stride or a pointer misses the alignment the kernels load with */
+  LSE_E_RANGE = -4,       /* K too large for exact int32 accumulation, or a size beyond int32 grids */
+  LSE_E_ALGO = -5,        /* unknown algorithm id, or one that cannot run this shape */
+};
+
+/* Algorithm selector for lse_w8a16_gemm_algo. */
+enum lse_algo {
+  LSE_ALGO_AUTO = 0,      /* decode kernel for M <= LSE_DECODE_MAX_M, prefill GEMM above */
+  LSE_ALGO_DECODE = 1,    /* streaming GEMV / skinny GEMM (M <= LSE_DECODE_MAX_M) */
+  LSE_ALGO_PREFILL = 2,   /* LDS-tiled MFMA GEMM */
+};
+
+/* lse_query keys. */
+enum lse_query_key {
+  LSE_Q_ABI_VERSION = 0,  /* this header's ABI version */
+  LSE_Q_K_ALIGN = 1,      /* K must be a multiple of this (bytes of an int8 row = elements) */
+  LSE_Q_DECODE_MAX_M = 2, /* largest M the decode kernel takes */
+  LSE_Q_MAX_K = 3,        /* largest K with exact int32 W8A8 accumulation */
+  LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
+};
+
+#define LSE_ABI_VERSION 1
+#define LSE_K_ALIGN 16
+#define LSE_DECODE_MAX_M 64
+#define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
+
+/*
+ * Per-output-channel symmetric weight quantization, run once at load time.
+ *   s[n] = fl32(max_k |w[n,k]| / 127)      (IEEE division; an all-zero row gets s[n] = 1)
+ *   q[n,k] = clamp(rne(fl32(w[n,k] / s[n])), -127, 127)
+ * w: (N, K) fp32, row stride ldw. q: (N, K) int8, contiguous (row stride K). s: (N) fp32.
+ * Replaces: the bf16 `nn.Linear.weight` that `AutoModelForCausalLM.from_pretrained` loads
+ * (model_runner.py:50-52) at the int8 switch (model_runner.py:45-46).
+ */
+int lse_quantize_weight_per_channel(const float* w, int64_t ldw, int8_t* q, float* s,
+                                    int64_t N, int64_t K, void* stream);
+
+/*
+ * W8A16 linear: y[m,n] = bf16_rne(s[n] * sum_k x[m,k] * q[n,k]), fp32 accumulation.
+ * x: (M, K) bf16, row stride ldx (multiple of 8, 16-byte aligned base).
+ * q: (N, K) int8 contiguous, K % LSE_K_ALIGN == 0. s: (N) fp32.
+ * y: (M, N) bf16, row stride ldy >= N (any; 8-byte stores are used when ldy % 4 == 0 and the
+ *    base is 8-byte aligned, 2-byte stores otherwise).
+ * Replaces: `F.linear(x, W)` of `nn.Linear.forward` (torch/nn/modules/linear.py:134) at
+ * model_runner.py:322-324, 369, 418 and modeling_llama.py:175 (LlamaMLP.forward).
+ */
+int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const float* s, void* y,
+                   int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* lse_w8a16_gemm with the kernel family chosen by the caller (enum lse_algo); used to test
+ * the decode and prefill kernels on identical inputs. Same contract otherwise. */
+int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* q, const float* s, void* y,
+                        int64_t ldy, int64_t M, int64_t N, int64_t K, int algo, void* stream);
+
+/*
+ * Dynamic per-token activation quantization (W8A8 first stage).
+ *   sx[m] = fl32(max_k |x[m,k]| / 127)     (an all-zero row gets sx[m] = 1)
+ *   xq[m,k] = clamp(rne(fl32(x[m,k] / sx[m])), -127, 127)
+ * x: (M, K) bf16, row stride ldx. xq: (M, K) int8 contiguous. sx: (M) fp32.
+ * Replaces: nothing in the reference; it is the activation half of the int8 path the switch at
+ * model_runner.py:45-46 names.
+ */
+int lse_quantize_act_per_token(const void* x, int64_t ldx, int8_t* xq, float* sx,
+                               int64_t M, int64_t K, void* stream);
+
+/*
+ * W8A8 linear: acc[m,n] = sum_k xq[m,k] * q[n,k] exactly in int32;
+ *   y[m,n] = bf16_rne((fp32(acc[m,n]) * sx[m]) * s[n]).
+ * xq: (M, K) int8 contiguous; q: (N, K) int8 contiguous; K % LSE_K_ALIGN == 0, K <= LSE_MAX_K.
+ * y: (M, N) bf16 with row stride ldy >= N, or NULL to skip it.
+ * acc: (M, N) int32 contiguous, or NULL to skip it (the bit-exact test reads it).
+ * Replaces: `F.linear(x, W)` (torch/nn/modules/linear.py:134) at the same call sites as
+ * lse_w8a16_gemm, in the dynamic per-token mode.
+ */
+int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s, void* y,
+                  int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Static properties (enum lse_query_key); -1 for an unknown key. Load-time checks read these,
+ * as `ModelRunner.check_custom_kernel_support` (model_runner.py:77-94) checks its kernels. */
+int64_t lse_query(int key);
+
+/* Text for a status code returned above (never NULL). */
+const char* lse_status_string(int status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LSE_INT8_H */

@@ -1,0 +1,164 @@
+// extern "C" entry points of liblse_int8.so (declared in include/lse_int8.h): argument checks,
+// then dispatch to the kernels. A rejected argument returns a negative status before anything is
+// launched; a launch failure returns the hipError_t.
+#include "lse_common.h"
+
+namespace lse {
+int launch_quantize_weight(const float* w, int64_t ldw, int8_t* q, float* s, int64_t N, int64_t K,
+                           hipStream_t stream);
+int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, int64_t M,
+                        int64_t K, hipStream_t stream);
+int launch_w8a16_decode(const uint16_t* x, int64_t ldx, const int8_t* q, const float* s,
+                        uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                        hipStream_t stream);
+int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* q, const float* s, uint16_t* y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s,
+                     uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
+                     hipStream_t stream);
+}  // namespace lse
+
+namespace {
+
+constexpr int64_t kMaxGridX = 2147483647;
+constexpr int64_t kMaxGridY = 65535;
+constexpr int64_t kMaxRows = 2147483647;  // row indices are int inside the kernels
+
+bool aligned(const void* p, uintptr_t bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+// Checks shared by every GEMM-shaped entry point: sizes, K alignment and range, scale vector.
+int check_common(const int8_t* q, const float* s, int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0 || M > kMaxRows || N > kMaxRows) return LSE_E_SHAPE;
+  if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
+  if (K > LSE_MAX_K) return LSE_E_RANGE;
+  if (M == 0 || N == 0) return LSE_OK;
+  if (!q || !s) return LSE_E_NULL;
+  if (!aligned(q, 16) || !aligned(s, 16)) return LSE_E_ALIGN;
+  return LSE_OK;
+}
+
+int check_bf16_matrix(const void* p, int64_t ld, int64_t rows, int64_t cols, int elem_align) {
+  if (rows == 0 || cols == 0) return LSE_OK;
+  if (!p) return LSE_E_NULL;
+  if (ld < cols) return LSE_E_SHAPE;
+  if (ld % elem_align || !aligned(p, 2 * elem_align)) return LSE_E_ALIGN;
+  return LSE_OK;
+}
+
+// y[m, :] = 0 when K == 0: the empty sum. Written as a plain kernel so the call stays
+// capture-safe (no memset node).
+__global__ void zero_rows(uint16_t* y, int64_t ldy, int64_t M, int64_t N) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < M * N) y[(i / N) * ldy + i % N] = 0;
+}
+
+int zero_output(void* y, int64_t ldy, int64_t M, int64_t N, hipStream_t stream) {
+  const int64_t total = M * N;
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > kMaxGridX) return LSE_E_RANGE;
+  hipLaunchKernelGGL(zero_rows, dim3((unsigned)blocks), dim3(256), 0, stream, (uint16_t*)y, ldy, M,
+                     N);
+  return lse::launch_status();
+}
+
+__global__ void zero_i32(int32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lse_quantize_weight_per_channel(const float* w, int64_t ldw, int8_t* q, float* s, int64_t N,
+                                    int64_t K, void* stream) {
+  if (N < 0 || K < 0 || N > kMaxGridX) return LSE_E_SHAPE;
+  if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
+  if (N == 0) return LSE_OK;
+  if (!s || (K > 0 && (!w || !q))) return LSE_E_NULL;
+  if (K > 0 && ldw < K) return LSE_E_SHAPE;
+  if (K > 0 && (ldw % 4 || !aligned(w, 16) || !aligned(q, 16))) return LSE_E_ALIGN;
+  return lse::launch_quantize_weight(w, ldw, q, s, N, K, (hipStream_t)stream);
+}
+
+int lse_quantize_act_per_token(const void* x, int64_t ldx, int8_t* xq, float* sx, int64_t M,
+                               int64_t K, void* stream) {
+  if (M < 0 || K < 0 || M > kMaxGridX) return LSE_E_SHAPE;
+  if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
+  if (M == 0) return LSE_OK;
+  if (!sx || (K > 0 && !xq)) return LSE_E_NULL;
+  if (int st = check_bf16_matrix(x, ldx, M, K, 8)) return st;
+  if (K > 0 && !aligned(xq, 16)) return LSE_E_ALIGN;
+  return lse::launch_quantize_act((const uint16_t*)x, ldx, xq, sx, M, K, (hipStream_t)stream);
+}
+
+int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* q, const float* s, void* y,
+                        int64_t ldy, int64_t M, int64_t N, int64_t K, int algo, void* stream) {
+  if (int st = check_common(q, s, M, N, K)) return st;
+  if (algo < LSE_ALGO_AUTO || algo > LSE_ALGO_PREFILL) return LSE_E_ALGO;
+  if (algo == LSE_ALGO_DECODE && M > LSE_DECODE_MAX_M) return LSE_E_ALGO;
+  if (M == 0 || N == 0) return LSE_OK;
+  if (int st = check_bf16_matrix(y, ldy, M, N, 1)) return st;
+  hipStream_t st = (hipStream_t)stream;
+  if (K == 0) return zero_output(y, ldy, M, N, st);
+  if (int e = check_bf16_matrix(x, ldx, M, K, 8)) return e;
+  if (algo == LSE_ALGO_AUTO) algo = M <= LSE_DECODE_MAX_M ? LSE_ALGO_DECODE : LSE_ALGO_PREFILL;
+  if (algo == LSE_ALGO_DECODE)
+    return lse::launch_w8a16_decode((const uint16_t*)x, ldx, q, s, (uint16_t*)y, ldy, M, N, K, st);
+  if ((M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
+  return lse::launch_w8a16_gemm((const uint16_t*)x, ldx, q, s, (uint16_t*)y, ldy, M, N, K, st);
+}
+
+int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const float* s, void* y,
+                   int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
+  return lse_w8a16_gemm_algo(x, ldx, q, s, y, ldy, M, N, K, LSE_ALGO_AUTO, stream);
+}
+
+int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s, void* y,
+                  int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream) {
+  if (int st = check_common(q, s, M, N, K)) return st;
+  if (M == 0 || N == 0) return LSE_OK;
+  if (!sx) return LSE_E_NULL;
+  if (y) {
+    if (int st = check_bf16_matrix(y, ldy, M, N, 1)) return st;
+  }
+  if (acc && !aligned(acc, 16)) return LSE_E_ALIGN;
+  hipStream_t st = (hipStream_t)stream;
+  if (K == 0) {
+    if (acc) {
+      hipLaunchKernelGGL(zero_i32, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, st, acc,
+                         M * N);
+      if (int e = lse::launch_status()) return e;
+    }
+    return y ? zero_output(y, ldy, M, N, st) : LSE_OK;
+  }
+  if (!xq) return LSE_E_NULL;
+  if (!aligned(xq, 16)) return LSE_E_ALIGN;
+  if (M > LSE_DECODE_MAX_M && (M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
+  return lse::launch_w8a8_gemm(xq, sx, q, s, (uint16_t*)y, ldy, acc, M, N, K, st);
+}
+
+int64_t lse_query(int key) {
+  switch (key) {
+    case LSE_Q_ABI_VERSION: return LSE_ABI_VERSION;
+    case LSE_Q_K_ALIGN: return LSE_K_ALIGN;
+    case LSE_Q_DECODE_MAX_M: return LSE_DECODE_MAX_M;
+    case LSE_Q_MAX_K: return LSE_MAX_K;
+    case LSE_Q_GFX_ARCH: return 950;
+    default: return -1;
+  }
+}
+
+const char* lse_status_string(int status) {
+  switch (status) {
+    case LSE_OK: return "ok";
+    case LSE_E_NULL: return "a required pointer is NULL";
+    case LSE_E_SHAPE: return "negative size or a stride smaller than its row";
+    case LSE_E_ALIGN: return "K, a stride or a pointer is not aligned as the kernels require";
+    case LSE_E_RANGE: return "size out of range (int32 accumulation or grid limits)";
+    case LSE_E_ALGO: return "unknown algorithm, or one that cannot run this shape";
+    default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
+  }
+}
+
+}  // extern "C"

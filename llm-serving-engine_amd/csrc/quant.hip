@@ -1,0 +1,105 @@
+// Row-wise symmetric int8 quantizers: per output channel for weights (load time) and per
+// token for activations (W8A8 first stage). Both compute, per row r,
+//   scale[r] = fl32(amax_r / 127)   (IEEE division; an all-zero row gets scale 1)
+//   out[r,k] = clamp(rne(fl32(v[r,k] / scale[r])), -127, 127)
+// with the correctly rounded fp32 division HIP compiles `/` to, so results are bit-exact
+// against any IEEE implementation of the same formula.
+#include "lse_common.h"
+
+namespace lse {
+
+constexpr int kQuantThreads = 256;
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < kQuantThreads / 64; ++w) m = fmaxf(m, red[w]);
+  return m;
+}
+
+__device__ __forceinline__ int8_t quant1(float v, float scale) {
+  const float t = __builtin_rintf(v / scale);
+  return (int8_t)fminf(fmaxf(t, -127.0f), 127.0f);
+}
+
+__device__ __forceinline__ float row_scale(float amax) { return amax > 0.0f ? amax / 127.0f : 1.0f; }
+
+// One workgroup per weight row; fp32 input read twice (the second pass hits L2).
+__global__ void __launch_bounds__(kQuantThreads)
+quantize_weight_rows(const float* __restrict__ w, int64_t ldw, int8_t* __restrict__ q,
+                     float* __restrict__ s, int K) {
+  __shared__ float red[kQuantThreads / 64];
+  const int64_t n = blockIdx.x;
+  const float* row = w + n * ldw;
+  float amax = 0.0f;
+  for (int k = threadIdx.x * 4; k < K; k += kQuantThreads * 4) {
+    const float4 v = *reinterpret_cast<const float4*>(row + k);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  const float scale = row_scale(block_max(amax, red));
+  if (threadIdx.x == 0) s[n] = scale;
+  int8_t* out = q + n * K;
+  for (int k = threadIdx.x * 4; k < K; k += kQuantThreads * 4) {
+    const float4 v = *reinterpret_cast<const float4*>(row + k);
+    const uint32_t packed = (uint32_t)(uint8_t)quant1(v.x, scale) |
+                            ((uint32_t)(uint8_t)quant1(v.y, scale) << 8) |
+                            ((uint32_t)(uint8_t)quant1(v.z, scale) << 16) |
+                            ((uint32_t)(uint8_t)quant1(v.w, scale) << 24);
+    *reinterpret_cast<uint32_t*>(out + k) = packed;
+  }
+}
+
+// One workgroup per token; bf16 input read twice (the second pass hits L2).
+__global__ void __launch_bounds__(kQuantThreads)
+quantize_act_rows(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ xq,
+                  float* __restrict__ sx, int K) {
+  __shared__ float red[kQuantThreads / 64];
+  const int64_t m = blockIdx.x;
+  const uint16_t* row = x + m * ldx;
+  float amax = 0.0f;
+  for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + k);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      amax = fmaxf(amax, fabsf(__builtin_bit_cast(float, w[i] << 16)));
+      amax = fmaxf(amax, fabsf(__builtin_bit_cast(float, w[i] & 0xffff0000u)));
+    }
+  }
+  const float scale = row_scale(block_max(amax, red));
+  if (threadIdx.x == 0) sx[m] = scale;
+  int8_t* out = xq + m * K;
+  for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + k);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, w[i] << 16), scale);
+      const uint32_t hi = (uint8_t)quant1(__builtin_bit_cast(float, w[i] & 0xffff0000u), scale);
+      packed[i >> 1] |= (lo | (hi << 8)) << (16 * (i & 1));
+    }
+    *reinterpret_cast<uint2*>(out + k) = make_uint2(packed[0], packed[1]);
+  }
+}
+
+int launch_quantize_weight(const float* w, int64_t ldw, int8_t* q, float* s, int64_t N, int64_t K,
+                           hipStream_t stream) {
+  hipLaunchKernelGGL(quantize_weight_rows, dim3((unsigned)N), dim3(kQuantThreads), 0, stream, w,
+                     ldw, q, s, (int)K);
+  return launch_status();
+}
+
+int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, int64_t M,
+                        int64_t K, hipStream_t stream) {
+  hipLaunchKernelGGL(quantize_act_rows, dim3((unsigned)M), dim3(kQuantThreads), 0, stream, x, ldx,
+                     xq, sx, (int)K);
+  return launch_status();
+}
+
+}  // namespace lse

@@ -1,0 +1,149 @@
+"""Tensor-level ops over the C ABI. Each validates dtypes, devices and layouts in Python,
+allocates its outputs with `torch.empty` (so CUDA-graph memory pools own them), and enqueues
+the HIP kernel on the current stream without synchronising, which keeps every op capturable
+into a graph.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "quantize_act_per_token",
+    "quantize_weight_per_channel",
+    "w8a8_linear",
+    "w8a16_linear",
+]
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _on_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    _require(dev.type == "cuda", f"int8 kernels need a CUDA (HIP) device, got {dev}")
+    for t in tensors[1:]:
+        _require(t.device == dev, f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _rows(x: torch.Tensor, k: int) -> torch.Tensor:
+    """(..., K) → a 2-D (rows, K) view whose last dim is contiguous."""
+    _require(x.shape[-1] == k, f"expected last dim {k}, got {tuple(x.shape)}")
+    x2 = x.reshape(-1, k)
+    strided_rows = x2.shape[0] > 1 and (x2.stride(0) < k or x2.stride(0) % 8)
+    if x2.stride(-1) != 1 or strided_rows or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2
+
+
+def quantize_weight_per_channel(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """W (N, K) → (q (N, K) int8, s (N,) fp32), s = amax/127 per row, q = clamp(rne(W/s)).
+
+    Runs on the GPU at load time. W is read as fp32 (bf16/fp16 weights widen exactly).
+    """
+    _require(w.dim() == 2, f"weight must be 2-D, got {tuple(w.shape)}")
+    dev = _on_gpu(w)
+    n, k = w.shape
+    w32 = w.to(torch.float32).contiguous()
+    q = torch.empty((n, k), dtype=torch.int8, device=dev)
+    s = torch.empty((n,), dtype=torch.float32, device=dev)
+    lib = _lib.library()
+    _lib.check(
+        lib.lse_quantize_weight_per_channel(
+            w32.data_ptr(), k, q.data_ptr(), s.data_ptr(), n, k, _stream(dev)
+        ),
+        "lse_quantize_weight_per_channel",
+    )
+    return q, s
+
+
+def w8a16_linear(
+    x: torch.Tensor,
+    qweight: torch.Tensor,
+    scales: torch.Tensor,
+    algo: int = _lib.ALGO_AUTO,
+) -> torch.Tensor:
+    """y = bf16(s[n] * sum_k x[..., k] q[n, k]) for x (..., K) bf16 → y (..., N) bf16."""
+    n, k = qweight.shape
+    dev = _on_gpu(x, qweight, scales)
+    _require(x.dtype == torch.bfloat16, f"W8A16 expects bf16 activations, got {x.dtype}")
+    _require(qweight.dtype == torch.int8 and qweight.is_contiguous(), "qweight must be contiguous int8")
+    _require(scales.dtype == torch.float32 and scales.shape == (n,), "scales must be fp32 (N,)")
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    ldx = x2.stride(0) if m > 1 else k
+    _lib.check(
+        _lib.library().lse_w8a16_gemm_algo(
+            x2.data_ptr(), ldx, qweight.data_ptr(), scales.data_ptr(), y.data_ptr(), n,
+            m, n, k, algo, _stream(dev),
+        ),
+        "lse_w8a16_gemm",
+    )
+    return y.view(*x.shape[:-1], n)
+
+
+def quantize_act_per_token(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """x (..., K) bf16 → (xq (rows, K) int8, sx (rows,) fp32), per-row symmetric int8."""
+    dev = _on_gpu(x)
+    _require(x.dtype == torch.bfloat16, f"W8A8 expects bf16 activations, got {x.dtype}")
+    k = x.shape[-1]
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    xq = torch.empty((m, k), dtype=torch.int8, device=dev)
+    sx = torch.empty((m,), dtype=torch.float32, device=dev)
+    ldx = x2.stride(0) if m > 1 else k
+    _lib.check(
+        _lib.library().lse_quantize_act_per_token(
+            x2.data_ptr(), ldx, xq.data_ptr(), sx.data_ptr(), m, k, _stream(dev)
+        ),
+        "lse_quantize_act_per_token",
+    )
+    return xq, sx
+
+
+def w8a8_gemm(
+    xq: torch.Tensor,
+    sx: torch.Tensor,
+    qweight: torch.Tensor,
+    scales: torch.Tensor,
+    want_acc: bool = False,
+    want_y: bool = True,
+) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """(y (M, N) bf16 or None, acc (M, N) int32 or None) from quantized operands."""
+    n, k = qweight.shape
+    dev = _on_gpu(xq, sx, qweight, scales)
+    m = xq.shape[0]
+    _require(xq.dtype == torch.int8 and xq.shape == (m, k) and xq.is_contiguous(), "xq must be (M, K) int8")
+    _require(sx.dtype == torch.float32 and sx.shape == (m,), "sx must be fp32 (M,)")
+    _require(qweight.dtype == torch.int8 and qweight.is_contiguous(), "qweight must be contiguous int8")
+    _require(scales.dtype == torch.float32 and scales.shape == (n,), "scales must be fp32 (N,)")
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev) if want_y else None
+    acc = torch.empty((m, n), dtype=torch.int32, device=dev) if want_acc else None
+    _lib.check(
+        _lib.library().lse_w8a8_gemm(
+            xq.data_ptr(), sx.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
+            y.data_ptr() if y is not None else None, n,
+            acc.data_ptr() if acc is not None else None, m, n, k, _stream(dev),
+        ),
+        "lse_w8a8_gemm",
+    )
+    return y, acc
+
+
+def w8a8_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """Dynamic per-token W8A8: quantize x per row, int8 GEMM with exact int32 accumulation,
+    y = bf16((acc * sx[m]) * s[n]). x (..., K) bf16 → y (..., N) bf16."""
+    n = qweight.shape[0]
+    xq, sx = quantize_act_per_token(x)
+    y, _ = w8a8_gemm(xq, sx, qweight, scales)
+    return y.view(*x.shape[:-1], n)

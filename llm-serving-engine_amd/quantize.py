@@ -1,0 +1,56 @@
+"""Swaps a loaded Llama-family model's projections for `Int8Linear`, in place.
+
+This is the work the reference's int8 switch stands in for: `ModelRunner.__init__` raises
+`NotImplementedError("int8 weight-only quantization")` before loading
+(src/llm_serving_engine/model/model_runner.py:45-46). The swap has to finish inside
+`ModelRunner.__init__`, after `from_pretrained(...).to(device)` (model_runner.py:50-52) and
+before any CUDA graph is captured (engine.py:94-106), because a graph freezes kernels and
+tensor addresses. lm_head stays bf16, as the reference's `emit_owed` computes it
+(model_runner.py:306-307).
+"""
+
+from __future__ import annotations
+
+import gc
+
+import torch
+from torch import nn
+
+from .int8_linear import MODES, Int8Linear
+
+ATTENTION_PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj")
+MLP_PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
+
+
+def check_int8_support(model: nn.Module) -> None:
+    """Load-time refusal, in the manner of `check_custom_kernel_support`
+    (model_runner.py:77-94): a Llama-family layout on a GPU in bf16."""
+    if not hasattr(model, "model") or not hasattr(model.model, "layers"):
+        raise RuntimeError(
+            f"int8 quantization assumes a Llama-family decoder (model.model.layers); "
+            f"{type(model).__name__} has no such attribute"
+        )
+    p = next(model.parameters())
+    if p.device.type != "cuda":
+        raise RuntimeError(f"int8 kernels need a CUDA (HIP) device, got {p.device}")
+    if p.dtype != torch.bfloat16:
+        raise RuntimeError(f"int8 kernels compute in bfloat16, the model is {p.dtype}")
+
+
+@torch.no_grad()
+def quantize_model_(model: nn.Module, mode: str = "int8") -> nn.Module:
+    """Replaces q/k/v/o and gate/up/down of every decoder layer by `Int8Linear` (per-channel
+    int8 weights quantized on the GPU). Returns the same model object."""
+    if mode not in MODES:
+        raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
+    check_int8_support(model)
+    for layer in model.model.layers:
+        for parent, names in ((layer.self_attn, ATTENTION_PROJECTIONS), (layer.mlp, MLP_PROJECTIONS)):
+            for name in names:
+                linear = getattr(parent, name)
+                if isinstance(linear, nn.Linear):
+                    setattr(parent, name, Int8Linear.from_linear(linear, mode))
+                    del linear
+    gc.collect()
+    torch.cuda.empty_cache()
+    return model

@@ -1,0 +1,145 @@
+"""CPU oracle for the int8 quantized Linear forward. TEST INFRASTRUCTURE ONLY.
+
+Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import
+this module, and then only as the checker. No product path routes through it. The product
+path runs hand-written HIP kernels and fails when their library is missing.
+
+The reference engine declares the path but does not implement it:
+`ModelConfig.quantize` (src/llm_serving_engine/config.py:32) selects "int8", and
+`ModelRunner.__init__` raises `NotImplementedError("int8 weight-only quantization")`
+(src/llm_serving_engine/model/model_runner.py:45-46). Only the layer being replaced carries
+arithmetic: `nn.Linear.forward` → `F.linear(x, W)` with bias=False for every Llama projection
+(torch/nn/modules/linear.py:130-134; transformers modeling_llama.py:163-175,230-241). The
+numerics below restate the quantized version of that layer as the benchmark configurations
+define it:
+
+* per-output-channel weights: s[n] = max_k |W[n,k]| / 127, q = clamp(rne(W / s), -127, 127);
+* W8A16: y[m,n] = bf16(s[n] * sum_k x[m,k] * q[n,k]), fp32 accumulation;
+* W8A8: sx[m] = max_k |x[m,k]| / 127, xq = clamp(rne(x / sx), -127, 127),
+  acc = sum_k xq * q exactly in int32, y = bf16((fp32(acc) * sx[m]) * s[n]).
+
+All-zero rows are not defined by the specification; this oracle fixes s = 1, q = 0.
+
+Every function is pinned by a check that does not retype it (hand-worked known answers,
+closed forms, brute force over exact rationals, torch's independent RNE cast and integer
+matmul); those checks live in tests/test_oracle.py.
+
+Dtypes on this boundary: bf16 tensors are carried as their uint16 bit patterns, so numpy
+(which has no bfloat16) round-trips them exactly.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+QMAX = 127
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns (uint16) → float32. Exact: bf16 is the top half of an fp32."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 → bf16 bit patterns, round-to-nearest-even on the dropped 16 bits.
+
+    NaN inputs stay NaN (quiet bit forced); infinities and overflow to infinity behave as the
+    IEEE rounding of the top half does.
+    """
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    rounded = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded)
+
+
+def f64_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float64 → bf16 via float32. Double rounding f64→f32→bf16 can differ from a direct
+    f64→bf16 rounding by one bf16 ulp; callers compare such values with a tolerance."""
+    return f32_to_bf16_bits(np.asarray(x, dtype=np.float64).astype(np.float32))
+
+
+def quantize_weight_per_channel(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """W (N,K) float32 → q (N,K) int8, s (N,) float32.
+
+    s[n] = fl32(amax_n / 127) with IEEE division; q = clamp(rne(fl32(W / s)), -127, 127).
+    An all-zero row gets s = 1, q = 0.
+    """
+    w = np.asarray(w, dtype=np.float32)
+    amax = np.max(np.abs(w), axis=1) if w.shape[1] else np.zeros(w.shape[0], np.float32)
+    s = np.where(amax > 0, amax / np.float32(QMAX), np.float32(1.0)).astype(np.float32)
+    q = np.clip(np.rint(w / s[:, None]), -QMAX, QMAX).astype(np.int8)
+    return q, s
+
+
+def quantize_act_per_token(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """x (M,K) bf16 bits → xq (M,K) int8, sx (M,) float32, the same rule as the weights but per
+    row of activations: sx[m] = fl32(max_k |x[m,k]| / 127), xq = clamp(rne(fl32(x / sx))).
+    An all-zero row gets sx = 1, xq = 0."""
+    return quantize_weight_per_channel(bf16_bits_to_f32(x_bits))
+
+
+def w8a16_golden(x_bits: np.ndarray, q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """fp64 golden of y = s[n] * sum_k x[m,k] q[n,k] (M,N). Every product x*q is exact in fp64
+    (8-bit by 8-bit significands) and the fp64 sum's error is far below bf16 resolution."""
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    return (x @ np.asarray(q, dtype=np.float64).T) * np.asarray(s, dtype=np.float64)[None, :]
+
+
+def w8a8_accumulate(xq: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """Exact int32 accumulators acc[m,n] = sum_k xq[m,k] q[n,k].
+
+    |acc| <= 127 * 127 * K, which stays below 2^31 for K < 133,144, so int64 arithmetic
+    followed by the int32 cast is exact for every shape the path accepts.
+    """
+    acc = np.asarray(xq, dtype=np.int64) @ np.asarray(q, dtype=np.int64).T
+    if acc.size and np.max(np.abs(acc)) >= 2**31:
+        raise OverflowError("int32 accumulator overflow")
+    return acc.astype(np.int32)
+
+
+def w8a8_epilogue(acc: np.ndarray, sx: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """y = bf16_rne((fp32(acc) * sx[m]) * s[n]), two fp32 roundings in this order."""
+    a = np.asarray(acc, dtype=np.int32).astype(np.float32)
+    y = (a * np.asarray(sx, np.float32)[:, None]) * np.asarray(s, np.float32)[None, :]
+    return f32_to_bf16_bits(y.astype(np.float32))
+
+
+def bf16_linear_cpu(x_bits: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """fp64 product x·Wᵀ of the unquantized layer (the reference's bf16 `F.linear`,
+    torch/nn/modules/linear.py:134), with W rounded to bf16 as the reference stores it."""
+    wb = bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(w, np.float32))).astype(np.float64)
+    return bf16_bits_to_f32(x_bits).astype(np.float64) @ wb.T
+
+
+def within_tolerance(y_bits: np.ndarray, golden: np.ndarray, rel: float = 1e-2) -> tuple[bool, str]:
+    """The W8A16 acceptance rule: max-abs error <= rel * max|golden|, and elementwise relative
+    error <= rel wherever |golden| > 1e-3 * max|golden|."""
+    y = bf16_bits_to_f32(y_bits).astype(np.float64)
+    g = np.asarray(golden, np.float64)
+    if g.size == 0:
+        return True, "empty"
+    if not np.all(np.isfinite(y)):
+        return False, "non-finite output"
+    gmax = float(np.max(np.abs(g)))
+    err = np.abs(y - g)
+    max_abs = float(np.max(err))
+    big = np.abs(g) > 1e-3 * gmax
+    max_rel = float(np.max(err[big] / np.abs(g[big]))) if np.any(big) else 0.0
+    ok = max_abs <= rel * max(gmax, 1e-30) and max_rel <= rel
+    return ok, f"max_abs={max_abs:.3e} (gmax={gmax:.3e}) max_rel={max_rel:.3e}"
+
+
+def seeded_inputs(
+    seed: int, m: int, n: int, k: int, outliers: bool = False
+) -> tuple[np.ndarray, np.ndarray]:
+    """x (M,K) bf16 bits ~ N(0,1) and W (N,K) float32 ~ N(0, 0.02) from one seeded generator.
+    With `outliers`, round(0.001*K) activation columns chosen by seeded permutation are
+    multiplied by 20 in fp32 before the bf16 rounding."""
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    if outliers:
+        cols = rng.permutation(k)[: int(round(0.001 * k))]
+        x[:, cols] *= np.float32(20.0)
+    return f32_to_bf16_bits(x), w

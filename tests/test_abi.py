@@ -1,0 +1,120 @@
+"""The C ABI without a GPU: the library loads, exports every function include/lse_int8.h declares,
+and rejects bad arguments with the documented status before any HIP call is made."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO_ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((REPO_ROOT / "include").glob("*.h"))
+
+
+def _declared_functions() -> set[str]:
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*[\w\s\*]*?\b(lse_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    assert {
+        "lse_quantize_weight_per_channel", "lse_w8a16_gemm", "lse_w8a16_gemm_algo",
+        "lse_quantize_act_per_token", "lse_w8a8_gemm", "lse_query", "lse_status_string",
+    } <= names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg.library()
+    exported = subprocess.run(
+        ["nm", "-D", "--defined-only", str(pkg.LIB_PATH)], capture_output=True, text=True, check=True
+    ).stdout
+    for name in _declared_functions():
+        assert re.search(rf"\bT {name}$", exported, flags=re.M), name
+        assert getattr(lib, name) is not None
+
+
+def test_binding_covers_the_header(pkg):
+    from llm_serving_engine_amd import _lib
+
+    assert set(_lib.SIGNATURES) == _declared_functions()
+
+
+def test_query_values(pkg):
+    from llm_serving_engine_amd import _lib
+
+    assert _lib.query(_lib.Q_ABI_VERSION) == _lib.ABI_VERSION
+    assert _lib.query(_lib.Q_K_ALIGN) == 16
+    assert _lib.query(_lib.Q_DECODE_MAX_M) == 64
+    assert 127 * 127 * _lib.query(_lib.Q_MAX_K) < 2**31
+    assert _lib.query(_lib.Q_GFX_ARCH) == 950
+    assert _lib.query(99) == -1
+
+
+# A fake, 256-byte-aligned device address: every call below is rejected before it is used.
+FAKE = ctypes.c_void_p(1 << 20)
+E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO = -1, -2, -3, -4, -5
+
+
+@pytest.mark.parametrize(
+    "args,status",
+    [
+        # (x, ldx, q, s, y, ldy, M, N, K, algo)
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 1, 64, 60, 0), E_ALIGN),  # K % 16
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, -1, 64, 64, 0), E_SHAPE),
+        ((FAKE, 64, None, FAKE, FAKE, 64, 1, 64, 64, 0), E_NULL),
+        ((FAKE, 64, FAKE, None, FAKE, 64, 1, 64, 64, 0), E_NULL),
+        ((FAKE, 64, FAKE, FAKE, None, 64, 1, 64, 64, 0), E_NULL),
+        ((None, 64, FAKE, FAKE, FAKE, 64, 1, 64, 64, 0), E_NULL),
+        ((FAKE, 60, FAKE, FAKE, FAKE, 64, 2, 64, 64, 0), E_SHAPE),  # ldx < K
+        ((FAKE, 68, FAKE, FAKE, FAKE, 64, 2, 64, 64, 0), E_ALIGN),  # ldx % 8
+        ((FAKE, 64, FAKE, FAKE, ctypes.c_void_p((1 << 20) + 1), 64, 2, 64, 64, 0), E_ALIGN),
+        ((FAKE, 64, FAKE, FAKE, FAKE, 32, 2, 64, 64, 0), E_SHAPE),  # ldy < N
+        ((ctypes.c_void_p((1 << 20) + 8), 64, FAKE, FAKE, FAKE, 64, 1, 64, 64, 0), E_ALIGN),
+        ((FAKE, 64, ctypes.c_void_p((1 << 20) + 4), FAKE, FAKE, 64, 1, 64, 64, 0), E_ALIGN),
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 65, 64, 64, 1), E_ALGO),  # decode takes M <= 64
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 1, 64, 64, 7), E_ALGO),
+        ((FAKE, 1 << 20, FAKE, FAKE, FAKE, 64, 1, 64, 200_000, 0), E_RANGE),
+    ],
+)
+def test_w8a16_rejects_bad_arguments(pkg, args, status):
+    lib = pkg.library()
+    assert lib.lse_w8a16_gemm_algo(*args, None) == status
+    assert lib.lse_status_string(status)
+
+
+def test_empty_shapes_are_no_ops(pkg):
+    lib = pkg.library()
+    assert lib.lse_w8a16_gemm(None, 0, None, None, None, 0, 0, 0, 0, None) == 0
+    assert lib.lse_w8a16_gemm(None, 16, FAKE, FAKE, None, 0, 0, 64, 16, None) == 0
+    assert lib.lse_w8a8_gemm(None, None, FAKE, FAKE, None, 0, None, 0, 64, 16, None) == 0
+    assert lib.lse_quantize_act_per_token(None, 0, None, FAKE, 0, 16, None) == 0
+    assert lib.lse_quantize_weight_per_channel(None, 0, None, FAKE, 0, 16, None) == 0
+
+
+def test_quantizers_and_w8a8_reject_bad_arguments(pkg):
+    lib = pkg.library()
+    assert lib.lse_quantize_weight_per_channel(FAKE, 64, FAKE, FAKE, 4, 40, None) == E_ALIGN
+    assert lib.lse_quantize_weight_per_channel(FAKE, 30, FAKE, FAKE, 4, 32, None) == E_SHAPE
+    assert lib.lse_quantize_weight_per_channel(FAKE, 34, FAKE, FAKE, 4, 32, None) == E_ALIGN
+    assert lib.lse_quantize_weight_per_channel(FAKE, 32, FAKE, None, 4, 32, None) == E_NULL
+    assert lib.lse_quantize_act_per_token(FAKE, 32, FAKE, FAKE, -1, 32, None) == E_SHAPE
+    assert lib.lse_quantize_act_per_token(FAKE, 36, FAKE, FAKE, 2, 32, None) == E_ALIGN
+    assert lib.lse_quantize_act_per_token(None, 32, FAKE, FAKE, 2, 32, None) == E_NULL
+    assert lib.lse_w8a8_gemm(FAKE, None, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, None) == E_NULL
+    assert lib.lse_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, FAKE, 64, None, 2, 64, 200_000, None) == E_RANGE
+    assert lib.lse_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, FAKE, 64, ctypes.c_void_p((1 << 20) + 4),
+                             2, 64, 64, None) == E_ALIGN
+    assert lib.lse_w8a8_gemm(None, FAKE, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, None) == E_NULL
+
+
+def test_status_strings(pkg):
+    lib = pkg.library()
+    for st in (0, E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO, -99):
+        assert isinstance(lib.lse_status_string(st), bytes)

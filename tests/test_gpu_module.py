@@ -1,0 +1,121 @@
+"""`Int8Linear` as the engine sees it: an `nn.Linear(bias=False)` replacement on the current
+stream, capturable into a CUDA (HIP) graph, swapped into a Llama model by `quantize_model_`."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from helpers import bf16_bits
+from oracle import numerics as ora
+
+pytestmark = pytest.mark.gpu
+
+
+def _linear(dev, k, n, seed, bias=False):
+    torch.manual_seed(seed)
+    lin = nn.Linear(k, n, bias=bias, dtype=torch.bfloat16, device=dev)
+    nn.init.normal_(lin.weight, std=0.02)
+    return lin
+
+
+@pytest.mark.parametrize("mode", ["int8", "w8a8"])
+@pytest.mark.parametrize("shape", [(1, 1, 256), (1, 7, 256), (1, 96, 256), (3, 5, 256)])
+def test_forward_matches_oracle(pkg, dev, mode, shape):
+    lin = _linear(dev, 256, 192, 0)
+    mod = pkg.Int8Linear.from_linear(lin, mode)
+    assert isinstance(mod.qweight, torch.Tensor) and not isinstance(mod.qweight, nn.Parameter)
+    x = torch.randn(*shape, device=dev).to(torch.bfloat16)
+    y = mod(x)
+    assert y.shape == (*shape[:-1], 192) and y.dtype == torch.bfloat16
+    q_ref, s_ref = ora.quantize_weight_per_channel(lin.weight.detach().float().cpu().numpy())
+    np.testing.assert_array_equal(mod.qweight.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(mod.scales.cpu().numpy(), s_ref)
+    x_bits = bf16_bits(x.reshape(-1, 256))
+    if mode == "int8":
+        ok, msg = ora.within_tolerance(bf16_bits(y.reshape(-1, 192)), ora.w8a16_golden(x_bits, q_ref, s_ref))
+        assert ok, msg
+    else:
+        xq, sx = ora.quantize_act_per_token(x_bits)
+        expect = ora.w8a8_epilogue(ora.w8a8_accumulate(xq, q_ref), sx, s_ref)
+        np.testing.assert_array_equal(bf16_bits(y.reshape(-1, 192)), expect)
+
+
+def test_bias_is_added(pkg, dev):
+    lin = _linear(dev, 64, 48, 1, bias=True)
+    mod = pkg.Int8Linear.from_linear(lin)
+    x = torch.randn(4, 64, device=dev).to(torch.bfloat16)
+    no_bias = pkg.ops.w8a16_linear(x, mod.qweight, mod.scales)
+    assert torch.equal(mod(x), no_bias + lin.bias.detach())
+
+
+def test_non_contiguous_input(pkg, dev):
+    lin = _linear(dev, 128, 64, 2)
+    mod = pkg.Int8Linear.from_linear(lin)
+    base = torch.randn(8, 256, device=dev).to(torch.bfloat16)
+    x = base[:, 64:192]  # row stride 256, offset 128 bytes
+    assert torch.equal(mod(x), mod(x.contiguous()))
+    xt = torch.randn(128, 8, device=dev).to(torch.bfloat16).t()  # last dim strided
+    assert torch.equal(mod(xt), mod(xt.contiguous()))
+
+
+def test_runs_on_the_current_stream_and_captures_into_a_graph(pkg, dev):
+    """Graph replay equals eager bitwise, replay after replay, with eager work between them."""
+    lin = _linear(dev, 512, 384, 3)
+    mods = [pkg.Int8Linear.from_linear(lin, "int8"), pkg.Int8Linear.from_linear(lin, "w8a8")]
+    for mod in mods:
+        static_x = torch.randn(16, 512, device=dev).to(torch.bfloat16)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                mod(static_x)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_y = mod(static_x)
+        for i in range(4):
+            static_x.copy_(torch.randn(16, 512, device=dev).to(torch.bfloat16))
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = mod(static_x)
+            torch.cuda.synchronize()
+            assert torch.equal(static_y, eager), f"replay {i} ({mod.mode})"
+
+
+def test_quantize_model_swaps_llama_projections(pkg, dev):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(0)
+    config = LlamaConfig(
+        vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+        num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64,
+        bos_token_id=None, eos_token_id=None, pad_token_id=None,
+    )
+    model = LlamaForCausalLM(config).to(device=dev, dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, 64, (1, 12), device=dev)
+    with torch.no_grad():
+        ref_logits = model(ids).logits.float()
+    pkg.quantize_model_(model, "int8")
+    for layer in model.model.layers:
+        for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            assert isinstance(getattr(layer.self_attn, name), pkg.Int8Linear)
+        for name in ("gate_proj", "up_proj", "down_proj"):
+            assert isinstance(getattr(layer.mlp, name), pkg.Int8Linear)
+    assert isinstance(model.lm_head, nn.Linear) and not isinstance(model.lm_head, pkg.Int8Linear)
+    assert next(model.parameters()).dtype == torch.bfloat16
+    with torch.no_grad():
+        logits = model(ids).logits.float()
+    err = (logits - ref_logits).abs().max().item()
+    assert err <= 0.05 * ref_logits.abs().max().item(), err
+
+
+def test_load_time_refusals(pkg, dev):
+    odd = nn.Linear(40, 16, bias=False, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(RuntimeError, match="in_features"):
+        pkg.Int8Linear.from_linear(odd)
+    fp16_model = nn.Module()
+    with pytest.raises(RuntimeError, match="Llama"):
+        pkg.quantize_model_(fp16_model)

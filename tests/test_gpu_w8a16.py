@@ -1,0 +1,186 @@
+"""W8A16 parity on the GPU: both kernel families (decode M <= 64, prefill GEMM) against the
+oracle on identical seeded inputs, through the C ABI.
+
+Tolerance (north star: rel <= 1e-2 after fp32 accumulation): max-abs error <= 1e-2 * max|golden|
+and elementwise relative error <= 1e-2 where |golden| > 1e-3 * max|golden|; golden in fp64.
+Expected error is one bf16 rounding (2^-9) plus fp32 accumulation (~K * 2^-24).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_bits, to_bf16_tensor
+from oracle import numerics as ora
+
+pytestmark = pytest.mark.gpu
+
+DECODE, PREFILL = 1, 2
+LLAMA_SHAPES = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]  # (K, N)
+
+
+def _run(pkg, dev, x_bits, q, s, algo, ldy_pad=0):
+    m, k = x_bits.shape
+    n = q.shape[0]
+    x = to_bf16_tensor(x_bits, dev)
+    qt = torch.from_numpy(q).to(dev)
+    st = torch.from_numpy(s).to(dev)
+    if ldy_pad:
+        sentinel = torch.full((m, n + ldy_pad), -7.0, dtype=torch.bfloat16, device=dev)
+        lib = pkg.library()
+        status = lib.lse_w8a16_gemm_algo(
+            x.data_ptr(), k, qt.data_ptr(), st.data_ptr(), sentinel.data_ptr(), n + ldy_pad,
+            m, n, k, algo, torch.cuda.current_stream().cuda_stream,
+        )
+        assert status == 0
+        torch.cuda.synchronize()
+        pad = sentinel[:, n:]
+        assert torch.all(pad == -7.0), "kernel wrote outside y's rows"
+        return bf16_bits(sentinel[:, :n])
+    y = pkg.ops.w8a16_linear(x, qt, st, algo=algo)
+    torch.cuda.synchronize()
+    return bf16_bits(y)
+
+
+def _check(pkg, dev, m, n, k, seed, algo):
+    x_bits, w = ora.seeded_inputs(seed, m, n, k)
+    q, s = ora.quantize_weight_per_channel(w)
+    y = _run(pkg, dev, x_bits, q, s, algo)
+    ok, msg = ora.within_tolerance(y, ora.w8a16_golden(x_bits, q, s))
+    assert ok, f"M={m} N={n} K={k} algo={algo}: {msg}"
+    return x_bits, q, s, y
+
+
+def test_config0_gemv(pkg, dev):
+    """Config 0: M=1, K=N=2048, seeded x ~ N(0,1) bf16, W ~ N(0, 0.02)."""
+    _check(pkg, dev, 1, 2048, 2048, 0, DECODE)
+
+
+@pytest.mark.parametrize("m", [1, 2, 7, 8, 15, 16, 17, 31, 32, 33, 48, 63, 64])
+def test_decode_all_m_tiles(pkg, dev, m):
+    _check(pkg, dev, m, 272, 1024, 100 + m, DECODE)
+
+
+@pytest.mark.parametrize(
+    "n,k", [(1, 16), (15, 48), (16, 64), (17, 80), (100, 112), (33, 2064), (64, 4096 + 48)]
+)
+def test_decode_ragged_shapes(pkg, dev, n, k):
+    """N not a multiple of 16, K tails of 16/48 past the 64-wide superstep."""
+    for m in (1, 5, 40):
+        _check(pkg, dev, m, n, k, 7 * n + k, DECODE)
+
+
+@pytest.mark.parametrize("m", [65, 100, 128, 129, 300])
+@pytest.mark.parametrize("n,k", [(128, 64), (200, 112), (96, 1040), (384, 2048)])
+def test_prefill_ragged_shapes(pkg, dev, m, n, k):
+    _check(pkg, dev, m, n, k, 3 * m + n + k, PREFILL)
+
+
+def test_prefill_small_m_matches_tolerance(pkg, dev):
+    """The prefill kernel also accepts M <= 64 (one partly filled block)."""
+    _check(pkg, dev, 5, 256, 512, 11, PREFILL)
+
+
+@pytest.mark.parametrize("algo", [DECODE, PREFILL])
+def test_unit_vector_selects_one_column(pkg, dev, algo):
+    """x = e_k makes y[:, n] the single product bf16(fl32(q[n,k] * s[n])) exactly."""
+    k, n = 256, 48
+    _, w = ora.seeded_inputs(5, 1, n, k)
+    q, s = ora.quantize_weight_per_channel(w)
+    cols = [0, 17, 100, 255]
+    x = np.zeros((len(cols), k), np.float32)
+    for i, c in enumerate(cols):
+        x[i, c] = 1.0
+    y = _run(pkg, dev, ora.f32_to_bf16_bits(x), q, s, algo)
+    expect = ora.f32_to_bf16_bits(q[:, cols].T.astype(np.float32) * s[None, :])
+    np.testing.assert_array_equal(y, expect)
+
+
+@pytest.mark.parametrize("algo", [DECODE, PREFILL])
+def test_unit_scale_small_integers_are_exact(pkg, dev, algo):
+    """With s = 1 and small integer x, every partial sum is an exact fp32 integer below 2^8·K,
+    and the bf16 rounding of the total is the only rounding."""
+    rng = np.random.default_rng(9)
+    m, n, k = 9, 40, 512
+    x = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    s = np.ones(n, np.float32)
+    y = _run(pkg, dev, ora.f32_to_bf16_bits(x), q, s, algo)
+    exact = x.astype(np.int64) @ q.astype(np.int64).T
+    np.testing.assert_array_equal(y, ora.f32_to_bf16_bits(exact.astype(np.float32)))
+
+
+@pytest.mark.parametrize("algo", [DECODE, PREFILL])
+def test_output_stride_guard_band(pkg, dev, algo):
+    """ldy > N: the columns between N and ldy keep their sentinel."""
+    x_bits, w = ora.seeded_inputs(21, 70 if algo == PREFILL else 9, 52, 320)
+    q, s = ora.quantize_weight_per_channel(w)
+    y = _run(pkg, dev, x_bits, q, s, algo, ldy_pad=12)
+    assert ora.within_tolerance(y, ora.w8a16_golden(x_bits, q, s))[0]
+
+
+def test_decode_rows_are_batch_invariant(pkg, dev):
+    """A row's result does not depend on M or on the other rows: the graphed decode runs a
+    padded bucket while eager decode runs the exact batch, and both must agree bitwise."""
+    x_bits, w = ora.seeded_inputs(31, 64, 512, 4096)
+    q, s = ora.quantize_weight_per_channel(w)
+    full = _run(pkg, dev, x_bits, q, s, DECODE)
+    for m in (1, 3, 16, 17, 37, 63):
+        part = _run(pkg, dev, x_bits[:m], q, s, DECODE)
+        np.testing.assert_array_equal(part, full[:m], err_msg=f"M={m}")
+    padded = x_bits.copy()
+    padded[40:] = 0
+    np.testing.assert_array_equal(_run(pkg, dev, padded, q, s, DECODE)[:40], full[:40])
+
+
+def test_prefill_rows_are_batch_invariant(pkg, dev):
+    x_bits, w = ora.seeded_inputs(32, 400, 256, 1024)
+    q, s = ora.quantize_weight_per_channel(w)
+    full = _run(pkg, dev, x_bits, q, s, PREFILL)
+    for m in (65, 128, 129, 257):
+        np.testing.assert_array_equal(_run(pkg, dev, x_bits[:m], q, s, PREFILL), full[:m])
+
+
+def test_repeat_calls_are_deterministic(pkg, dev):
+    x_bits, w = ora.seeded_inputs(33, 64, 1024, 2048)
+    q, s = ora.quantize_weight_per_channel(w)
+    for algo in (DECODE, PREFILL):
+        a = _run(pkg, dev, x_bits, q, s, algo)
+        b = _run(pkg, dev, x_bits, q, s, algo)
+        np.testing.assert_array_equal(a, b)
+
+
+def _torch_fp32_reference(x, q, s):
+    """Plain PyTorch fp32 reference of the same op on the GPU: dequantize, fp32 GEMM."""
+    return (x.float() @ q.float().t()) * s[None, :]
+
+
+@pytest.mark.parametrize("k,n", LLAMA_SHAPES)
+def test_llama_decode_shapes_full_size(pkg, dev, k, n):
+    """Config 1 at full size: M in {1, 8, 32, 64} against a torch fp32 reference on the GPU,
+    and the weight quantizer against the oracle's digest-free invariants."""
+    gen = torch.Generator(device="cpu").manual_seed(1000 + k + n)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
+    q, s = pkg.ops.quantize_weight_per_channel(w)
+    for m in (1, 8, 32, 64):
+        x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+        y = pkg.ops.w8a16_linear(x, q, s, algo=DECODE)
+        ref = _torch_fp32_reference(x, q, s).double().cpu().numpy()
+        ok, msg = ora.within_tolerance(bf16_bits(y), ref)
+        assert ok, f"M={m} K={k} N={n}: {msg}"
+
+
+@pytest.mark.parametrize("k,n", LLAMA_SHAPES)
+def test_llama_prefill_shapes_full_size(pkg, dev, k, n):
+    """Config 2 at M=512 and 2048 (8192 is covered by the bench) vs torch fp32 on the GPU."""
+    gen = torch.Generator(device="cpu").manual_seed(2000 + k + n)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
+    q, s = pkg.ops.quantize_weight_per_channel(w)
+    for m in (512, 2048):
+        x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+        y = pkg.ops.w8a16_linear(x, q, s, algo=PREFILL)
+        ref = _torch_fp32_reference(x, q, s).double().cpu().numpy()
+        ok, msg = ora.within_tolerance(bf16_bits(y), ref)
+        assert ok, f"M={m} K={k} N={n}: {msg}"

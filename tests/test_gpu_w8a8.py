@@ -1,0 +1,99 @@
+"""W8A8 parity on the GPU: int32 accumulators bit-exact, the (acc * sx) * s epilogue bit-exact,
+for the decode (M <= 64) and tiled (M > 64) kernels, against the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_bits, to_bf16_tensor
+from oracle import numerics as ora
+
+pytestmark = pytest.mark.gpu
+
+LLAMA_SHAPES = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]  # (K, N)
+
+
+def _w8a8(pkg, dev, x_bits, q, s):
+    x = to_bf16_tensor(x_bits, dev)
+    xq, sx = pkg.ops.quantize_act_per_token(x)
+    y, acc = pkg.ops.w8a8_gemm(xq, sx, torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), True)
+    torch.cuda.synchronize()
+    return xq.cpu().numpy(), sx.cpu().numpy(), acc.cpu().numpy(), bf16_bits(y)
+
+
+def _check(pkg, dev, m, n, k, seed):
+    x_bits, w = ora.seeded_inputs(seed, m, n, k, outliers=True)
+    q, s = ora.quantize_weight_per_channel(w)
+    xq, sx, acc, y = _w8a8(pkg, dev, x_bits, q, s)
+    xq_ref, sx_ref = ora.quantize_act_per_token(x_bits)
+    np.testing.assert_array_equal(xq, xq_ref)
+    np.testing.assert_array_equal(sx, sx_ref)
+    acc_ref = ora.w8a8_accumulate(xq_ref, q)
+    np.testing.assert_array_equal(acc, acc_ref, err_msg=f"acc M={m} N={n} K={k}")
+    np.testing.assert_array_equal(y, ora.w8a8_epilogue(acc_ref, sx_ref, s), err_msg=f"y M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 16, 17, 32, 33, 64])
+def test_decode_kernel_bit_exact(pkg, dev, m):
+    _check(pkg, dev, m, 208, 1024, 500 + m)
+
+
+@pytest.mark.parametrize("m", [65, 128, 200, 512])
+@pytest.mark.parametrize("n,k", [(128, 128), (100, 176), (256, 2048)])
+def test_tiled_kernel_bit_exact(pkg, dev, m, n, k):
+    _check(pkg, dev, m, n, k, m + n + k)
+
+
+@pytest.mark.parametrize("n,k", [(1, 16), (17, 48), (45, 1072)])
+def test_ragged_shapes_bit_exact(pkg, dev, n, k):
+    for m in (1, 40, 90):
+        _check(pkg, dev, m, n, k, 13 * n + k + m)
+
+
+def test_extreme_operands_accumulate_exactly(pkg, dev):
+    """All-±127 operands at K = 14336: |acc| = 127^2 K = 231,225,344 is the largest magnitude the
+    Llama shapes reach, and it must land in int32 exactly."""
+    k, n = 14336, 32
+    xq = np.full((70, k), 127, np.int8)
+    xq[1::2] = -127
+    q = np.full((n, k), 127, np.int8)
+    q[::3] = -127
+    sx = np.ones(70, np.float32)
+    s = np.ones(n, np.float32)
+    for m in (5, 70):
+        y, acc = pkg.ops.w8a8_gemm(
+            torch.from_numpy(xq[:m].copy()).to(dev), torch.from_numpy(sx[:m].copy()).to(dev),
+            torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), True,
+        )
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(acc.cpu().numpy(), ora.w8a8_accumulate(xq[:m], q))
+
+
+@pytest.mark.parametrize("k,n", LLAMA_SHAPES)
+def test_llama_shapes_full_size(pkg, dev, k, n):
+    """Config 3 at full size for M in {1, 32, 512}: accumulators checked exactly with an fp64
+    GEMM on the GPU (integer products and sums below 2^53 are exact in fp64)."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    x_bits, w = ora.seeded_inputs(3000 + k + n, 512, n, k, outliers=True)
+    q, s = pkg.ops.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    for m in (1, 32, 512):
+        xq, sx = pkg.ops.quantize_act_per_token(to_bf16_tensor(x_bits[:m], dev))
+        y, acc = pkg.ops.w8a8_gemm(xq, sx, q, s, True)
+        exact = (xq.double() @ q.double().t()).round().to(torch.int64)
+        assert torch.equal(acc.to(torch.int64), exact), f"M={m} K={k} N={n}"
+        y_ref = ora.w8a8_epilogue(acc.cpu().numpy(), sx.cpu().numpy(), s.cpu().numpy())
+        np.testing.assert_array_equal(bf16_bits(y), y_ref)
+
+
+def test_acc_only_and_y_only(pkg, dev):
+    x_bits, w = ora.seeded_inputs(61, 20, 64, 256, outliers=True)
+    q, s = ora.quantize_weight_per_channel(w)
+    xq, sx = pkg.ops.quantize_act_per_token(to_bf16_tensor(x_bits, dev))
+    qt, st = torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)
+    y_only, none_acc = pkg.ops.w8a8_gemm(xq, sx, qt, st, want_acc=False, want_y=True)
+    none_y, acc_only = pkg.ops.w8a8_gemm(xq, sx, qt, st, want_acc=True, want_y=False)
+    assert none_acc is None and none_y is None
+    y_both, acc_both = pkg.ops.w8a8_gemm(xq, sx, qt, st, want_acc=True, want_y=True)
+    assert torch.equal(acc_only, acc_both) and torch.equal(y_only, y_both)

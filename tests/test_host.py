@@ -1,0 +1,88 @@
+"""Host-side logic without a GPU: the config switch, the module's buffers and its load-time
+refusals (mirroring the reference's int8 switch, config.py:32, and the RuntimeErrors of
+check_custom_kernel_support, model_runner.py:77-94)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from torch import nn
+
+
+def test_config_reads_the_reference_env_names(pkg, monkeypatch):
+    monkeypatch.setenv("LLM_QUANTIZE", "int8")
+    monkeypatch.setenv("LLM_DTYPE", "bfloat16")
+    monkeypatch.setenv("LLM_USE_CUDA_GRAPHS", "0")
+    cfg = pkg.ModelConfig.from_env()
+    assert (cfg.quantize, cfg.dtype, cfg.use_cuda_graphs) == ("int8", "bfloat16", False)
+    cfg.validate_quantize()
+
+
+def test_config_defaults_match_the_reference(pkg):
+    cfg = pkg.ModelConfig()
+    assert cfg.quantize == "none" and cfg.dtype == "float16" and cfg.device == "cuda"
+    cfg.validate_quantize()
+
+
+def test_config_refuses_unknown_mode_and_non_bf16(pkg):
+    with pytest.raises(ValueError):
+        pkg.ModelConfig(quantize="int4").validate_quantize()
+    with pytest.raises(RuntimeError, match="bfloat16"):
+        pkg.ModelConfig(quantize="int8", dtype="float16").validate_quantize()
+
+
+def test_int8_linear_holds_buffers_not_parameters(pkg):
+    mod = pkg.Int8Linear(64, 32, mode="w8a8", bias=True)
+    assert list(mod.parameters()) == []
+    names = dict(mod.named_buffers())
+    assert names["qweight"].dtype == torch.int8 and names["qweight"].shape == (32, 64)
+    assert names["scales"].dtype == torch.float32 and names["scales"].shape == (32,)
+    assert names["bias"].dtype == torch.bfloat16
+    assert "mode=w8a8" in repr(mod)
+    with pytest.raises(ValueError):
+        pkg.Int8Linear(64, 32, mode="fp8")
+
+
+def test_state_dict_round_trip(pkg):
+    a = pkg.Int8Linear(32, 16)
+    a.qweight.random_(-127, 128)
+    a.scales.uniform_()
+    b = pkg.Int8Linear(32, 16)
+    b.load_state_dict(a.state_dict())
+    assert torch.equal(a.qweight, b.qweight) and torch.equal(a.scales, b.scales)
+
+
+def test_cpu_forward_fails_loudly(pkg):
+    mod = pkg.Int8Linear(32, 16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        mod(torch.zeros(2, 32, dtype=torch.bfloat16))
+
+
+def test_from_linear_refuses_cpu_weights(pkg):
+    with pytest.raises(RuntimeError, match="CUDA"):
+        pkg.Int8Linear.from_linear(nn.Linear(32, 16, bias=False))
+
+
+def test_quantize_model_refuses_non_llama_and_cpu(pkg):
+    with pytest.raises(RuntimeError, match="Llama"):
+        pkg.quantize_model_(nn.Sequential(nn.Linear(16, 16)))
+
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    config = LlamaConfig(
+        vocab_size=32, hidden_size=32, intermediate_size=64, num_hidden_layers=1,
+        num_attention_heads=4, num_key_value_heads=2,
+    )
+    model = LlamaForCausalLM(config)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        pkg.quantize_model_(model)
+    with pytest.raises(ValueError):
+        pkg.quantize_model_(model, mode="int4")
+
+
+def test_ops_refuse_wrong_dtypes_before_touching_the_device(pkg):
+    x = torch.zeros(2, 32, dtype=torch.float16)
+    q = torch.zeros(16, 32, dtype=torch.int8)
+    s = torch.ones(16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        pkg.ops.w8a16_linear(x, q, s)

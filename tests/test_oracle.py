@@ -1,0 +1,283 @@
+"""Pins the CPU oracle (oracle/numerics.py) before anything is checked against it.
+
+The reference holds no golden vectors or known-answer tests for this path (its int8 switch
+raises NotImplementedError, src/llm_serving_engine/model/model_runner.py:45-46, pinned by
+tests/test_model_runner.py:120-122), so each oracle function is pinned here by something that
+does not restate it:
+* hand-worked known answers (exact scales 1 and 2, ties that separate round-half-even from
+  round-half-away);
+* exact rational arithmetic (fractions.Fraction) with an explicit IEEE round-to-nearest-even,
+  standing in for fp32 division and multiplication;
+* independent library routines: torch's bf16 cast, torch._int_mm, aten._weight_int8pack_mm;
+* brute force over tiny shapes, and planted mistakes that the acceptance rule must reject.
+"""
+
+from __future__ import annotations
+
+import json
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as ora
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def round_to_precision(v: Fraction, p: int) -> Fraction:
+    """v rounded to p significant bits, ties to even (normal range only)."""
+    if v == 0:
+        return Fraction(0)
+    sign = -1 if v < 0 else 1
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp = Fraction(2) ** (e - (p - 1))
+    t = a / ulp
+    n = t.numerator // t.denominator
+    r = t - n
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return sign * n * ulp
+
+
+def fl32(v: Fraction) -> Fraction:
+    return round_to_precision(v, 24)
+
+
+def rne_int(v: Fraction) -> int:
+    n = v.numerator // v.denominator
+    r = v - n
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return n
+
+
+# ---- bf16 rounding -------------------------------------------------------------------------
+
+
+def test_bf16_rounding_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(1e3),
+        np.array([0.0, -0.0, 1.0, np.inf, -np.inf, 3.3895314e38, 1e-40, -1e-45], np.float32),
+        # exact ties: low 16 bits 0x8000 with even and odd kept parts
+        np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x7F7F8000], np.uint32).view(np.float32),
+    ])
+    ours = ora.f32_to_bf16_bits(vals)
+    theirs = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(ours, theirs)
+    assert np.isnan(ora.bf16_bits_to_f32(ora.f32_to_bf16_bits(np.array([np.nan], np.float32))))[0]
+
+
+def test_bf16_roundtrip_is_exact():
+    bits = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16)
+    finite = np.isfinite(ora.bf16_bits_to_f32(bits))
+    np.testing.assert_array_equal(ora.f32_to_bf16_bits(ora.bf16_bits_to_f32(bits))[finite], bits[finite])
+
+
+# ---- weight quantizer ----------------------------------------------------------------------
+
+
+def test_weight_quant_known_answers():
+    w = np.zeros((4, 5), np.float32)
+    w[0] = [127.0, 63.5, -1.0, 0.5, 2.5]  # amax 127 → s = 1 exactly; ties go to even
+    w[1] = [254.0, -3.0, 5.0, 1.0, -254.0]  # s = 2 exactly; -1.5 → -2, 2.5 → 2, 0.5 → 0
+    w[3] = [0.0, 0.0, 0.0, 0.0, -0.25]  # s = fl32(0.25/127)
+    q, s = ora.quantize_weight_per_channel(w)
+    assert s[0] == 1.0 and s[1] == 2.0 and s[2] == 1.0
+    np.testing.assert_array_equal(q[0], [127, 64, -1, 0, 2])
+    np.testing.assert_array_equal(q[1], [127, -2, 2, 0, -127])
+    np.testing.assert_array_equal(q[2], 0)  # all-zero row: s = 1, q = 0
+    np.testing.assert_array_equal(q[3], [0, 0, 0, 0, -127])
+    assert Fraction(float(s[3])) == fl32(Fraction(1, 4) / 127)
+
+
+def test_weight_quant_matches_exact_rational_ieee():
+    """s = fl32(amax/127) and q = rne(fl32(w/s)) computed with exact rationals."""
+    _, w = ora.seeded_inputs(123, 1, 6, 40)
+    q, s = ora.quantize_weight_per_channel(w)
+    for n in range(w.shape[0]):
+        amax = max(abs(Fraction(float(v))) for v in w[n])
+        s_exact = fl32(amax / 127)
+        assert Fraction(float(s[n])) == s_exact
+        for k in range(w.shape[1]):
+            t = fl32(Fraction(float(w[n, k])) / s_exact)
+            assert q[n, k] == max(-127, min(127, rne_int(t))), (n, k)
+
+
+def test_weight_quant_invariants_at_scale():
+    _, w = ora.seeded_inputs(7, 1, 512, 4096)
+    q, s = ora.quantize_weight_per_channel(w)
+    assert q.dtype == np.int8 and s.dtype == np.float32 and q.shape == w.shape
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    np.testing.assert_array_equal(np.abs(q.astype(np.int32)).max(axis=1), 127)
+    # |q s - W| <= s/2, plus the fp32 rounding of W/s (half an ulp of |W/s| <= 127 is 2^-18 in
+    # units of s) and of s itself (2^-24 relative, times |q| <= 127): 2^-16 covers both.
+    err = np.abs(q.astype(np.float64) * s[:, None] - w.astype(np.float64))
+    assert np.all(err <= s[:, None].astype(np.float64) * (0.5 + 2.0**-16))
+
+
+# ---- activation quantizer ------------------------------------------------------------------
+
+
+def test_act_quant_known_answers_and_outliers():
+    x = np.zeros((3, 4), np.float32)
+    x[0] = [1.0, -0.5, 0.25, 0.0]  # amax 1: s = fl32(1/127)
+    x[2] = [-2.0, 2.0, 127.0, -127.0]  # amax 127: s = 1, exact
+    xq, sx = ora.quantize_act_per_token(ora.f32_to_bf16_bits(x))
+    assert Fraction(float(sx[0])) == fl32(Fraction(1, 127))
+    for k, v in enumerate(x[0]):
+        assert xq[0, k] == rne_int(fl32(Fraction(float(v)) / Fraction(float(sx[0]))))
+    np.testing.assert_array_equal(xq[0], [127, -64, 32, 0])
+    assert sx[1] == 1.0 and not xq[1].any()
+    np.testing.assert_array_equal(xq[2], [-2, 2, 127, -127])
+    x_bits, _ = ora.seeded_inputs(3, 8, 1, 4096, outliers=True)
+    xf = ora.bf16_bits_to_f32(x_bits)
+    big = np.abs(xf).max(axis=0) > 8.0
+    assert 1 <= big.sum() <= 4  # round(0.001 * 4096) = 4 outlier columns, x20
+
+
+def test_outlier_columns_count():
+    for k, expected in ((2048, 2), (4096, 4), (14336, 14)):
+        x_plain, _ = ora.seeded_inputs(5, 64, 1, k)
+        x_out, _ = ora.seeded_inputs(5, 64, 1, k, outliers=True)
+        changed = np.any(x_plain != x_out, axis=0)
+        assert changed.sum() == expected
+
+
+# ---- W8A16 golden --------------------------------------------------------------------------
+
+
+def test_w8a16_golden_brute_force_rational():
+    x_bits, w = ora.seeded_inputs(11, 3, 5, 32)
+    q, s = ora.quantize_weight_per_channel(w)
+    g = ora.w8a16_golden(x_bits, q, s)
+    xf = ora.bf16_bits_to_f32(x_bits)
+    for m in range(3):
+        for n in range(5):
+            exact = Fraction(float(s[n])) * sum(
+                Fraction(float(xf[m, k])) * int(q[n, k]) for k in range(32)
+            )
+            assert abs(Fraction(float(g[m, n])) - exact) <= abs(exact) * Fraction(1, 2**50)
+
+
+def test_w8a16_golden_unit_vector():
+    _, w = ora.seeded_inputs(12, 1, 8, 64)
+    q, s = ora.quantize_weight_per_channel(w)
+    x = np.zeros((1, 64), np.float32)
+    x[0, 9] = 1.0
+    g = ora.w8a16_golden(ora.f32_to_bf16_bits(x), q, s)
+    np.testing.assert_array_equal(g[0], q[:, 9].astype(np.float64) * s.astype(np.float64))
+
+
+def test_w8a16_golden_agrees_with_torch_dequantized_linear():
+    """torch's own fp64 F.linear on the dequantized weight (q·s applied before the sum, the
+    other association) agrees to fp64 rounding. aten._weight_int8pack_mm would be the closer
+    library routine, but this image's CPU build of it segfaults on some inputs."""
+    x_bits, w = ora.seeded_inputs(13, 4, 96, 512)
+    q, s = ora.quantize_weight_per_channel(w)
+    x = torch.from_numpy(x_bits.view(np.int16)).view(torch.bfloat16).double()
+    w_deq = torch.from_numpy(q).double() * torch.from_numpy(s).double()[:, None]
+    y = torch.nn.functional.linear(x, w_deq).numpy()
+    g = ora.w8a16_golden(x_bits, q, s)
+    np.testing.assert_allclose(g, y, rtol=1e-12, atol=1e-12 * np.abs(g).max())
+
+
+def test_tolerance_rule_rejects_planted_mistakes():
+    """Plausible kernel bugs, planted in the oracle's output on the CPU, all fail the rule."""
+    x_bits, w = ora.seeded_inputs(14, 8, 64, 1024)
+    q, s = ora.quantize_weight_per_channel(w)
+    g = ora.w8a16_golden(x_bits, q, s)
+    good = ora.f64_to_bf16_bits(g)
+    assert ora.within_tolerance(good, g)[0]
+    dropped = ora.f64_to_bf16_bits(ora.w8a16_golden(x_bits[:, :-16], q[:, :-16], s))  # lost K tail
+    wrong_scale = ora.f64_to_bf16_bits(g / s[None, :] * s[::-1][None, :])  # scale of another row
+    transposed_tile = good.copy()
+    transposed_tile[:4, :4] = good[:4, :4].T
+    sign = good ^ np.uint16(0x8000)
+    for bad in (dropped, wrong_scale, transposed_tile, sign):
+        assert not ora.within_tolerance(bad, g)[0]
+
+
+# ---- W8A8 ----------------------------------------------------------------------------------
+
+
+def test_w8a8_accumulate_matches_int_mm_and_loops():
+    rng = np.random.default_rng(15)
+    xq = rng.integers(-127, 128, (33, 128)).astype(np.int8)
+    q = rng.integers(-127, 128, (40, 128)).astype(np.int8)
+    acc = ora.w8a8_accumulate(xq, q)
+    ref = torch._int_mm(torch.from_numpy(xq), torch.from_numpy(q).t().contiguous()).numpy()
+    np.testing.assert_array_equal(acc, ref)
+    for m, n in ((0, 0), (5, 7), (32, 39)):
+        assert acc[m, n] == sum(int(xq[m, k]) * int(q[n, k]) for k in range(128))
+
+
+def test_w8a8_accumulate_extremes_and_overflow_guard():
+    k = 14336
+    a = np.full((1, k), 127, np.int8)
+    b = np.full((2, k), -127, np.int8)
+    assert ora.w8a8_accumulate(a, b)[0, 0] == -127 * 127 * k
+    with pytest.raises(OverflowError):
+        big = 133_200
+        ora.w8a8_accumulate(np.full((1, big), 127, np.int8), np.full((1, big), 127, np.int8))
+
+
+def test_w8a8_epilogue_order_is_pinned():
+    """y = bf16(fl32(fl32(acc * sx) * s)); checked with exact rationals on values where the two
+    association orders round differently."""
+    rng = np.random.default_rng(16)
+    acc = rng.integers(-2**24, 2**24, (6, 7)).astype(np.int32)
+    sx = (rng.random(6).astype(np.float32) * np.float32(0.03)).astype(np.float32)
+    s = (rng.random(7).astype(np.float32) * np.float32(0.002)).astype(np.float32)
+    y = ora.w8a8_epilogue(acc, sx, s)
+    differs = 0
+    for m in range(6):
+        for n in range(7):
+            a = Fraction(int(acc[m, n]))
+            left = fl32(fl32(a * Fraction(float(sx[m]))) * Fraction(float(s[n])))
+            right = fl32(a * fl32(Fraction(float(sx[m])) * Fraction(float(s[n]))))
+            expect = round_to_precision(left, 8)
+            assert Fraction(float(ora.bf16_bits_to_f32(y[m:m + 1, n])[0])) == expect
+            differs += left != right
+    assert differs > 0  # the pinned order is observable on these inputs
+
+
+# ---- committed fixtures --------------------------------------------------------------------
+
+
+def test_oracle_reproduces_committed_fixtures():
+    """tests/golden/*.npz were written by tests/golden/make_golden.py from this oracle; a change
+    to the oracle's numerics shows up here."""
+    with np.load(GOLDEN / "small_cases.npz") as f:
+        q, s = ora.quantize_weight_per_channel(f["w"])
+        np.testing.assert_array_equal(q, f["q"])
+        np.testing.assert_array_equal(s, f["s"])
+        np.testing.assert_array_equal(ora.w8a16_golden(f["x"], q, s), f["y_w8a16"])
+        xq, sx = ora.quantize_act_per_token(f["xo"])
+        np.testing.assert_array_equal(xq, f["xq"])
+        np.testing.assert_array_equal(sx, f["sx"])
+        acc = ora.w8a8_accumulate(xq, q)
+        np.testing.assert_array_equal(acc, f["acc"])
+        np.testing.assert_array_equal(ora.w8a8_epilogue(acc, sx, s), f["y_w8a8"])
+
+
+def test_config0_digests():
+    import hashlib
+
+    digests = json.loads((GOLDEN / "config0_digests.json").read_text())
+    x_bits, w = ora.seeded_inputs(0, 1, 2048, 2048)
+    q, s = ora.quantize_weight_per_channel(w)
+    y = ora.f64_to_bf16_bits(ora.w8a16_golden(x_bits, q, s))
+    got = {
+        name: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+        for name, a in (("x_bits", x_bits), ("q", q), ("s", s), ("y_bits", y))
+    }
+    assert got == digests
