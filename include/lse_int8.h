@@ -21,8 +21,12 @@
  *  - Return value: LSE_OK (0) on success; a negative LSE_E_* code for a rejected argument
  *    (nothing was launched); a positive hipError_t from the launch otherwise.
  *  - Results are deterministic: no atomics, and the reduction order of every output element
- *    depends only on K (not on M, N, or the other rows), so row m of y is bit-identical whether
- *    it is computed alone or inside a padded batch of any size up to the same kernel family.
+ *    depends only on K and on the token class of the call (M <= 16, 16 < M <= 64, M > 64), never
+ *    on N, on the other rows or on the grid. Row m of y is therefore bit-identical whether it
+ *    is computed alone or inside a padded batch of any size in the same class. The classes
+ *    align with power-of-two decode buckets: bucket(M) <= 16 exactly when M <= 16, and
+ *    bucket(M) <= 64 exactly when M <= 64, so a graphed bucket and the eager batch it stands
+ *    for always compute each row identically.
  */
 #ifndef LSE_INT8_H
 #define LSE_INT8_H

@@ -1,6 +1,10 @@
 // extern "C" entry points of liblse_int8.so (declared in include/lse_int8.h): argument checks,
 // then dispatch to the kernels. A rejected argument returns a negative status before anything is
 // launched; a launch failure returns the hipError_t.
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
 #include "lse_common.h"
 
 namespace lse {
@@ -18,11 +22,42 @@ int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const f
                      hipStream_t stream);
 }  // namespace lse
 
+namespace lse {
+
+int persistent_blocks(const void* kernel, int threads, size_t dyn_lds) {
+  struct Entry {
+    int device;
+    const void* kernel;
+    size_t dyn_lds;
+    int blocks;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 1;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Entry& e : cache)
+    if (e.device == device && e.kernel == kernel && e.dyn_lds == dyn_lds) return e.blocks;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, dyn_lds) !=
+          hipSuccess) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  const int blocks = std::max(1, cus * std::max(1, per_cu));
+  cache.push_back({device, kernel, dyn_lds, blocks});
+  return blocks;
+}
+
+}  // namespace lse
+
 namespace {
 
 constexpr int64_t kMaxGridX = 2147483647;
 constexpr int64_t kMaxGridY = 65535;
 constexpr int64_t kMaxRows = 2147483647;  // row indices are int inside the kernels
+constexpr uint32_t kBufferLimit = lse::kOutOfRange;  // byte extent of a buffer resource
 
 bool aligned(const void* p, uintptr_t bytes) { return ((uintptr_t)p % bytes) == 0; }
 
@@ -102,7 +137,12 @@ int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* q, const float
   hipStream_t st = (hipStream_t)stream;
   if (K == 0) return zero_output(y, ldy, M, N, st);
   if (int e = check_bf16_matrix(x, ldx, M, K, 8)) return e;
-  if (algo == LSE_ALGO_AUTO) algo = M <= LSE_DECODE_MAX_M ? LSE_ALGO_DECODE : LSE_ALGO_PREFILL;
+  // The decode kernel addresses x and q through 32-bit buffer resources.
+  const bool x_fits = ((M - 1) * ldx + K) * 2 < (int64_t)kBufferLimit &&
+                      (N + 16) * K < (int64_t)kBufferLimit;
+  if (algo == LSE_ALGO_AUTO)
+    algo = M <= LSE_DECODE_MAX_M && x_fits ? LSE_ALGO_DECODE : LSE_ALGO_PREFILL;
+  if (algo == LSE_ALGO_DECODE && !x_fits) return LSE_E_RANGE;
   if (algo == LSE_ALGO_DECODE)
     return lse::launch_w8a16_decode((const uint16_t*)x, ldx, q, s, (uint16_t*)y, ldy, M, N, K, st);
   if ((M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;

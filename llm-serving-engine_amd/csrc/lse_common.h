@@ -54,6 +54,29 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
 
+// Raw buffer resource (gfx9 descriptor: base, byte count, dword3 = 0x00020000). A buffer load
+// whose byte offset lies at or past the byte count returns zeros and issues no memory request;
+// the kernels use this for every ragged edge instead of branching around loads.
+typedef __amdgpu_buffer_rsrc_t BufferRsrc;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // past every resource (byte counts < 2^31)
+
+__device__ __forceinline__ BufferRsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(BufferRsrc r, uint32_t byte_offset) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Workgroups of `kernel` (launched with `threads` threads and `dyn_lds` bytes of dynamic LDS)
+// that fit on the current device at once: CU count x resident workgroups per CU. Persistent
+// kernels size their grid with it. Cached per (device, kernel, dyn_lds); host-side queries only,
+// so it is safe during stream capture.
+int persistent_blocks(const void* kernel, int threads, size_t dyn_lds = 0);
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LSE_OK : (int)e;

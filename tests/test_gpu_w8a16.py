@@ -121,18 +121,30 @@ def test_output_stride_guard_band(pkg, dev, algo):
     assert ora.within_tolerance(y, ora.w8a16_golden(x_bits, q, s))[0]
 
 
-def test_decode_rows_are_batch_invariant(pkg, dev):
-    """A row's result does not depend on M or on the other rows: the graphed decode runs a
-    padded bucket while eager decode runs the exact batch, and both must agree bitwise."""
-    x_bits, w = ora.seeded_inputs(31, 64, 512, 4096)
+@pytest.mark.parametrize("k", [4096, 14336])
+def test_decode_rows_are_batch_invariant(pkg, dev, k):
+    """A row's result does not depend on M or on the other rows within a token class (M <= 16,
+    16 < M <= 64): the graphed decode runs a padded power-of-two bucket while eager decode runs
+    the exact batch, and bucket(M) <= 16 exactly when M <= 16, so both land in one class and
+    must agree bitwise. Across the class boundary rows agree to the tolerance."""
+    x_bits, w = ora.seeded_inputs(31, 64, 512, k)
     q, s = ora.quantize_weight_per_channel(w)
     full = _run(pkg, dev, x_bits, q, s, DECODE)
-    for m in (1, 3, 16, 17, 37, 63):
+    small = _run(pkg, dev, x_bits[:16], q, s, DECODE)
+    for m in (1, 3, 8, 15):
+        part = _run(pkg, dev, x_bits[:m], q, s, DECODE)
+        np.testing.assert_array_equal(part, small[:m], err_msg=f"M={m}")
+    for m in (17, 32, 37, 63):
         part = _run(pkg, dev, x_bits[:m], q, s, DECODE)
         np.testing.assert_array_equal(part, full[:m], err_msg=f"M={m}")
     padded = x_bits.copy()
     padded[40:] = 0
     np.testing.assert_array_equal(_run(pkg, dev, padded, q, s, DECODE)[:40], full[:40])
+    padded16 = x_bits[:16].copy()
+    padded16[5:] = 0
+    np.testing.assert_array_equal(_run(pkg, dev, padded16, q, s, DECODE)[:5], small[:5])
+    golden = ora.w8a16_golden(x_bits[:16], q, s)
+    assert ora.within_tolerance(full[:16], golden)[0] and ora.within_tolerance(small, golden)[0]
 
 
 def test_prefill_rows_are_batch_invariant(pkg, dev):
