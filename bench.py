@@ -51,14 +51,16 @@ def parse() -> argparse.Namespace:
 
 
 def make_weights(pkg, dev, k: int, n: int, copies: int, gen):
-    """`copies` independent (q, s) pairs, quantized on the GPU from W ~ N(0, 0.02)."""
+    """`copies` independent (packed q, s) pairs, quantized and packed on the GPU from
+    W ~ N(0, 0.02)."""
     import torch
 
     out = []
     for _ in range(copies):
         w = (torch.randn(n, k, generator=gen, device="cpu") * 0.02).to(dev)
-        out.append(pkg.ops.quantize_weight_per_channel(w))
-        del w
+        q, s = pkg.ops.quantize_weight_per_channel(w)
+        out.append((pkg.ops.pack_weight(q), s))
+        del w, q
     return out
 
 

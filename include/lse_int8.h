@@ -13,6 +13,10 @@
  * Conventions shared by every entry point:
  *  - All pointers are device pointers. The caller owns every buffer; the library keeps no state
  *    beyond its compiled kernels and allocates nothing.
+ *  - Weights travel in the packed tile layout written by lse_pack_weight: tiles of 16 rows x 64
+ *    K-bytes, 1 KB each, tile (rb, j) at byte (rb * ceil(K/64) + j) * 1024, its byte 16*l + i
+ *    holding q[16*rb + l%16][64*j + 16*(l/16) + i], zero past N and K. One 128-bit load per lane
+ *    of a 64-wide wave reads one tile, contiguous and already in matrix-core operand order.
  *  - Matrices are row-major. `ld*` is the row stride in elements. bf16 data travels as
  *    `void*` (2 bytes per element, IEEE bfloat16 bit patterns).
  *  - `stream` is a `hipStream_t` passed as `void*`. Work is enqueued on it and never
@@ -20,13 +24,13 @@
  *    accepted but callers that capture must pass their capture stream.
  *  - Return value: LSE_OK (0) on success; a negative LSE_E_* code for a rejected argument
  *    (nothing was launched); a positive hipError_t from the launch otherwise.
- *  - Results are deterministic: no atomics, and the reduction order of every output element
- *    depends only on K and on the token class of the call (M <= 16, 16 < M <= 64, M > 64), never
- *    on N, on the other rows or on the grid. Row m of y is therefore bit-identical whether it
- *    is computed alone or inside a padded batch of any size in the same class. The classes
- *    align with power-of-two decode buckets: bucket(M) <= 16 exactly when M <= 16, and
- *    bucket(M) <= 64 exactly when M <= 64, so a graphed bucket and the eager batch it stands
- *    for always compute each row identically.
+ *  - Results are deterministic: no atomics, and the summation order of every output element
+ *    depends only on N, K, the device's CU count and the token class of the call (M <= 16,
+ *    17..32, 33..64, > 64), never on M inside the class, on other rows or on timing. Row m of y
+ *    is therefore bit-identical whether it is computed alone or inside a padded batch of the
+ *    same class. The classes align with power-of-two decode buckets (bucket(M) <= 16 exactly
+ *    when M <= 16, and so on), so a graphed bucket and the eager batch it stands for compute
+ *    each row identically.
  */
 #ifndef LSE_INT8_H
 #define LSE_INT8_H
@@ -62,7 +66,7 @@ enum lse_query_key {
   LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
 };
 
-#define LSE_ABI_VERSION 1
+#define LSE_ABI_VERSION 2
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -78,21 +82,33 @@ enum lse_query_key {
 int lse_quantize_weight_per_channel(const float* w, int64_t ldw, int8_t* q, float* s,
                                     int64_t N, int64_t K, void* stream);
 
+/* Bytes of the packed layout of an (N, K) weight: ceil(N/16) * ceil(K/64) * 1024. */
+int64_t lse_packed_weight_bytes(int64_t N, int64_t K);
+
+/*
+ * Packs a row-major (N, K) int8 weight (contiguous, K % LSE_K_ALIGN == 0, 16-byte aligned) into
+ * the tile layout every GEMM below reads (qp: lse_packed_weight_bytes(N, K) bytes, 16-byte
+ * aligned). Load time only.
+ * Replaces: nothing in the reference (its weights are row-major `nn.Linear.weight`); it is the
+ * storage step of the int8 switch (model_runner.py:45-46).
+ */
+int lse_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, void* stream);
+
 /*
  * W8A16 linear: y[m,n] = bf16_rne(s[n] * sum_k x[m,k] * q[n,k]), fp32 accumulation.
  * x: (M, K) bf16, row stride ldx (multiple of 8, 16-byte aligned base).
- * q: (N, K) int8 contiguous, K % LSE_K_ALIGN == 0. s: (N) fp32.
+ * qp: packed (N, K) int8 weight, K % LSE_K_ALIGN == 0. s: (N) fp32.
  * y: (M, N) bf16, row stride ldy >= N (any; 8-byte stores are used when ldy % 4 == 0 and the
  *    base is 8-byte aligned, 2-byte stores otherwise).
  * Replaces: `F.linear(x, W)` of `nn.Linear.forward` (torch/nn/modules/linear.py:134) at
  * model_runner.py:322-324, 369, 418 and modeling_llama.py:175 (LlamaMLP.forward).
  */
-int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const float* s, void* y,
+int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
                    int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* lse_w8a16_gemm with the kernel family chosen by the caller (enum lse_algo); used to test
  * the decode and prefill kernels on identical inputs. Same contract otherwise. */
-int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* q, const float* s, void* y,
+int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
                         int64_t ldy, int64_t M, int64_t N, int64_t K, int algo, void* stream);
 
 /*
@@ -109,13 +125,13 @@ int lse_quantize_act_per_token(const void* x, int64_t ldx, int8_t* xq, float* sx
 /*
  * W8A8 linear: acc[m,n] = sum_k xq[m,k] * q[n,k] exactly in int32;
  *   y[m,n] = bf16_rne((fp32(acc[m,n]) * sx[m]) * s[n]).
- * xq: (M, K) int8 contiguous; q: (N, K) int8 contiguous; K % LSE_K_ALIGN == 0, K <= LSE_MAX_K.
- * y: (M, N) bf16 with row stride ldy >= N, or NULL to skip it.
+ * xq: (M, K) int8 contiguous; qp: packed (N, K) int8 weight; K % LSE_K_ALIGN == 0,
+ * K <= LSE_MAX_K. y: (M, N) bf16 with row stride ldy >= N, or NULL to skip it.
  * acc: (M, N) int32 contiguous, or NULL to skip it (the bit-exact test reads it).
  * Replaces: `F.linear(x, W)` (torch/nn/modules/linear.py:134) at the same call sites as
  * lse_w8a16_gemm, in the dynamic per-token mode.
  */
-int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s, void* y,
+int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* y,
                   int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Static properties (enum lse_query_key); -1 for an unknown key. Load-time checks read these,

@@ -12,9 +12,14 @@ int launch_quantize_weight(const float* w, int64_t ldw, int8_t* q, float* s, int
                            hipStream_t stream);
 int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, int64_t M,
                         int64_t K, hipStream_t stream);
-int launch_w8a16_decode(const uint16_t* x, int64_t ldx, const int8_t* q, const float* s,
+int launch_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, hipStream_t stream);
+int64_t packed_weight_bytes(int64_t N, int64_t K);
+int launch_w8a16_skinny(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
                         uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                         hipStream_t stream);
+int launch_w8a8_skinny(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                       uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
+                       hipStream_t stream);
 int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* q, const float* s, uint16_t* y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s,
@@ -101,6 +106,11 @@ __global__ void zero_i32(int32_t* p, int64_t n) {
   if (i < n) p[i] = 0;
 }
 
+// The packed weight and the 32-bit buffer offsets the kernels address it with.
+int check_packed(int64_t N, int64_t K) {
+  return lse::packed_weight_bytes(N, K) < (int64_t)kBufferLimit ? LSE_OK : LSE_E_RANGE;
+}
+
 }  // namespace
 
 extern "C" {
@@ -127,9 +137,24 @@ int lse_quantize_act_per_token(const void* x, int64_t ldx, int8_t* xq, float* sx
   return lse::launch_quantize_act((const uint16_t*)x, ldx, xq, sx, M, K, (hipStream_t)stream);
 }
 
-int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* q, const float* s, void* y,
+int64_t lse_packed_weight_bytes(int64_t N, int64_t K) {
+  if (N < 0 || K < 0) return -1;
+  return lse::packed_weight_bytes(N, K);
+}
+
+int lse_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, void* stream) {
+  if (N < 0 || K < 0 || N > kMaxRows) return LSE_E_SHAPE;
+  if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
+  if (N == 0 || K == 0) return LSE_OK;
+  if (!q || !qp) return LSE_E_NULL;
+  if (!aligned(q, 16) || !aligned(qp, 16)) return LSE_E_ALIGN;
+  if (int st = check_packed(N, K)) return st;
+  return lse::launch_pack_weight(q, N, K, qp, (hipStream_t)stream);
+}
+
+int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
                         int64_t ldy, int64_t M, int64_t N, int64_t K, int algo, void* stream) {
-  if (int st = check_common(q, s, M, N, K)) return st;
+  if (int st = check_common(qp, s, M, N, K)) return st;
   if (algo < LSE_ALGO_AUTO || algo > LSE_ALGO_PREFILL) return LSE_E_ALGO;
   if (algo == LSE_ALGO_DECODE && M > LSE_DECODE_MAX_M) return LSE_E_ALGO;
   if (M == 0 || N == 0) return LSE_OK;
@@ -137,26 +162,25 @@ int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* q, const float
   hipStream_t st = (hipStream_t)stream;
   if (K == 0) return zero_output(y, ldy, M, N, st);
   if (int e = check_bf16_matrix(x, ldx, M, K, 8)) return e;
-  // The decode kernel addresses x and q through 32-bit buffer resources.
-  const bool x_fits = ((M - 1) * ldx + K) * 2 < (int64_t)kBufferLimit &&
-                      (N + 16) * K < (int64_t)kBufferLimit;
-  if (algo == LSE_ALGO_AUTO)
-    algo = M <= LSE_DECODE_MAX_M && x_fits ? LSE_ALGO_DECODE : LSE_ALGO_PREFILL;
-  if (algo == LSE_ALGO_DECODE && !x_fits) return LSE_E_RANGE;
-  if (algo == LSE_ALGO_DECODE)
-    return lse::launch_w8a16_decode((const uint16_t*)x, ldx, q, s, (uint16_t*)y, ldy, M, N, K, st);
+  if (int e = check_packed(N, K)) return e;
+  if (algo == LSE_ALGO_AUTO) algo = M <= LSE_DECODE_MAX_M ? LSE_ALGO_DECODE : LSE_ALGO_PREFILL;
+  if (algo == LSE_ALGO_DECODE) {
+    // The decode kernel addresses x through a 32-bit buffer resource.
+    if (((M - 1) * ldx + K) * 2 >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+    return lse::launch_w8a16_skinny((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K, st);
+  }
   if ((M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
-  return lse::launch_w8a16_gemm((const uint16_t*)x, ldx, q, s, (uint16_t*)y, ldy, M, N, K, st);
+  return lse::launch_w8a16_gemm((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K, st);
 }
 
-int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const float* s, void* y,
+int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
                    int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
-  return lse_w8a16_gemm_algo(x, ldx, q, s, y, ldy, M, N, K, LSE_ALGO_AUTO, stream);
+  return lse_w8a16_gemm_algo(x, ldx, qp, s, y, ldy, M, N, K, LSE_ALGO_AUTO, stream);
 }
 
-int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s, void* y,
+int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* y,
                   int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream) {
-  if (int st = check_common(q, s, M, N, K)) return st;
+  if (int st = check_common(qp, s, M, N, K)) return st;
   if (M == 0 || N == 0) return LSE_OK;
   if (!sx) return LSE_E_NULL;
   if (y) {
@@ -174,8 +198,13 @@ int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const floa
   }
   if (!xq) return LSE_E_NULL;
   if (!aligned(xq, 16)) return LSE_E_ALIGN;
-  if (M > LSE_DECODE_MAX_M && (M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
-  return lse::launch_w8a8_gemm(xq, sx, q, s, (uint16_t*)y, ldy, acc, M, N, K, st);
+  if (int e = check_packed(N, K)) return e;
+  if (M <= LSE_DECODE_MAX_M) {
+    if (M * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+    return lse::launch_w8a8_skinny(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, st);
+  }
+  if ((M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
+  return lse::launch_w8a8_gemm(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, st);
 }
 
 int64_t lse_query(int key) {

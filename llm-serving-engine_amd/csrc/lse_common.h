@@ -71,6 +71,22 @@ __device__ __forceinline__ uint4 buffer_load16(BufferRsrc r, uint32_t byte_offse
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+__device__ __forceinline__ i32x4 mfma_i8(uint4 a, uint4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a),
+                                               __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+
+// Packed weight layout. The (N, K) int8 matrix is cut into tiles of 16 rows x 64 K-bytes; tile
+// (rb, j) is 1024 contiguous bytes at ((rb * nsteps) + j) * 1024, nsteps = ceil(K / 64), and its
+// byte 16 * l + i holds q[16 * rb + l % 16][64 * j + 16 * (l / 16) + i] (zero past N or K). One
+// 128-bit load per lane of a wave reads one whole tile, already in MFMA operand order: lane l
+// holds 16 K-consecutive bytes of row l % 16.
+constexpr int kTileRows = 16;
+constexpr int kTileK = 64;
+constexpr int kTileBytes = 1024;
+
+__host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
 // Workgroups of `kernel` (launched with `threads` threads and `dyn_lds` bytes of dynamic LDS)
 // that fit on the current device at once: CU count x resident workgroups per CU. Persistent
 // kernels size their grid with it. Cached per (device, kernel, dyn_lds); host-side queries only,

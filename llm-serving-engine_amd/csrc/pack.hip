@@ -1,0 +1,37 @@
+// Row-major (N, K) int8 weight -> packed tiles of 16 rows x 64 K-bytes (layout in lse_common.h).
+// One thread writes one 16-byte lane slot of a tile: 16 K-consecutive bytes of one row, which is
+// one aligned 128-bit load from the row-major source (K % 16 == 0). Rows past N and K past the
+// end are written as zeros, so the GEMMs can read whole tiles without edge cases.
+#include "lse_common.h"
+
+namespace lse {
+
+__global__ void __launch_bounds__(256)
+pack_weight_tiles(const int8_t* __restrict__ q, int N, int K, int nsteps, int64_t slots,
+                  uint4* __restrict__ qp) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= slots) return;
+  const int64_t tile = t >> 6;
+  const int lane = (int)(t & 63);
+  const int64_t rb = tile / nsteps;
+  const int j = (int)(tile - rb * nsteps);
+  const int64_t row = 16 * rb + (lane & 15);
+  const int k = 64 * j + 16 * (lane >> 4);
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (row < N && k < K) v = *reinterpret_cast<const uint4*>(q + row * K + k);
+  qp[t] = v;
+}
+
+int64_t packed_weight_bytes(int64_t N, int64_t K) {
+  return ceil_div(N, kTileRows) * ceil_div(K, kTileK) * kTileBytes;
+}
+
+int launch_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, hipStream_t stream) {
+  const int64_t slots = packed_weight_bytes(N, K) / 16;
+  const int64_t blocks = ceil_div(slots, 256);
+  hipLaunchKernelGGL(pack_weight_tiles, dim3((unsigned)blocks), dim3(256), 0, stream, q, (int)N,
+                     (int)K, (int)ceil_div(K, kTileK), slots, reinterpret_cast<uint4*>(qp));
+  return launch_status();
+}
+
+}  // namespace lse

@@ -2,7 +2,8 @@
 //
 // MFMA-bound. A block computes a BM x BN tile of y over K in BK steps:
 //  * x (bf16) and q (int8) tiles travel global → registers (128-bit loads) → LDS, double
-//    buffered, so the next tile's loads are in flight while the current tile is multiplied.
+//    buffered, so the next tile's loads are in flight while the current tile is multiplied. q
+//    comes from the packed layout: a block step reads eight whole 1 KB tiles.
 //  * q is dequantized to bf16 on its way into LDS, once per block (not once per wave).
 //  * Each wave owns a WM x WN sub-tile built from v_mfma_f32_16x16x32_bf16, fp32 accumulate.
 //  * Epilogue: scale by s[n] (fp32) and round to bf16 once.
@@ -50,15 +51,19 @@ w8a16_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __r
     a_lds[i] = row * LDK + kc * 8;
     a_k[i] = kc * 8;
   }
-  const int8_t* b_src[B_CHUNKS];
-  int b_lds[B_CHUNKS], b_k[B_CHUNKS];
+  // Chunk c is lane slot c % 64 of tile n_block / 16 + c / 64 at the block's K step: row
+  // 16 * (c / 64) + l % 16 of the block, K offset 16 * (l / 16).
+  const int nsteps = (K + 63) / 64;
+  const uint4* b_src[B_CHUNKS];
+  int b_lds[B_CHUNKS];
+  bool b_ok[B_CHUNKS];
 #pragma unroll
   for (int i = 0; i < B_CHUNKS; ++i) {
-    const int c = tid + THREADS * i;
-    const int row = c / (BK / 16), kc = c % (BK / 16);
-    b_src[i] = q + (int64_t)min(n_block + row, N - 1) * K + kc * 16;
-    b_lds[i] = row * LDK + kc * 16;
-    b_k[i] = kc * 16;
+    const int c = tid + THREADS * i, t = c / 64, l = c % 64;
+    const int rb = n_block / 16 + t;
+    b_ok[i] = rb < (N + 15) / 16;
+    b_src[i] = reinterpret_cast<const uint4*>(q) + (int64_t)(b_ok[i] ? rb : 0) * nsteps * 64 + l;
+    b_lds[i] = (16 * t + (l & 15)) * LDK + 16 * (l >> 4);
   }
 
   uint4 a_reg[A_CHUNKS], b_reg[B_CHUNKS];
@@ -70,8 +75,7 @@ w8a16_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __r
                                            : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < B_CHUNKS; ++i)
-      b_reg[i] = (full || k0 + b_k[i] < K) ? *reinterpret_cast<const uint4*>(b_src[i] + k0)
-                                           : make_uint4(0, 0, 0, 0);
+      b_reg[i] = b_ok[i] ? b_src[i][(int64_t)(k0 / 64) * 64] : make_uint4(0, 0, 0, 0);
   };
   auto store_tile = [&](int buf) {
 #pragma unroll

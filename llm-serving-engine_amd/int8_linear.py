@@ -6,6 +6,9 @@ modeling_llama.py:175), so the replacement keeps exactly `forward(x) -> y` with 
 y (..., N) in bf16 on the same device and the current stream. Quantized weights and scales are
 buffers, not Parameters: the runner reads `model.dtype` off the first parameter
 (model_runner.py:86,112) and must keep seeing bf16.
+
+`qweight` holds the int8 weight in the packed tile layout the kernels stream (ops.pack_weight),
+shape (ceil(N/16), ceil(K/64), 1024); `unpacked_qweight()` returns the row-major (N, K) matrix.
 """
 
 from __future__ import annotations
@@ -38,7 +41,8 @@ class Int8Linear(nn.Module):
         self.out_features = out_features
         self.mode = mode
         self.register_buffer(
-            "qweight", torch.zeros((out_features, in_features), dtype=torch.int8, device=device)
+            "qweight",
+            torch.zeros(ops.packed_shape(out_features, in_features), dtype=torch.int8, device=device),
         )
         self.register_buffer("scales", torch.ones((out_features,), dtype=torch.float32, device=device))
         self.register_buffer(
@@ -52,7 +56,8 @@ class Int8Linear(nn.Module):
         w = linear.weight.detach()
         mod = cls(linear.in_features, linear.out_features, mode, linear.bias is not None, w.device)
         q, s = ops.quantize_weight_per_channel(w)
-        mod.qweight.copy_(q)
+        mod.qweight.copy_(ops.pack_weight(q))
+        del q
         mod.scales.copy_(s)
         if linear.bias is not None:
             mod.bias.copy_(linear.bias.detach().to(torch.bfloat16))
@@ -63,14 +68,19 @@ class Int8Linear(nn.Module):
         cls, qweight: torch.Tensor, scales: torch.Tensor, mode: str = "int8",
         bias: torch.Tensor | None = None,
     ) -> Int8Linear:
-        """Wraps already quantized (N, K) int8 weights and (N,) fp32 scales."""
+        """Wraps already quantized row-major (N, K) int8 weights and (N,) fp32 scales (on the GPU;
+        they are packed there)."""
         n, k = qweight.shape
         mod = cls(k, n, mode, bias is not None, qweight.device)
-        mod.qweight.copy_(qweight)
+        mod.qweight.copy_(ops.pack_weight(qweight))
         mod.scales.copy_(scales)
         if bias is not None:
             mod.bias.copy_(bias.to(torch.bfloat16))
         return mod
+
+    def unpacked_qweight(self) -> torch.Tensor:
+        """The int8 weight as a row-major (N, K) matrix."""
+        return ops.unpack_weight(self.qweight, self.out_features, self.in_features)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.mode == "int8":

@@ -2,6 +2,10 @@
 allocates its outputs with `torch.empty` (so CUDA-graph memory pools own them), and enqueues
 the HIP kernel on the current stream without synchronising, which keeps every op capturable
 into a graph.
+
+Weights are held in the packed tile layout the kernels stream (`pack_weight`): a (N, K) int8
+matrix becomes a (ceil(N/16), ceil(K/64), 1024) int8 tensor whose 1 KB tiles are 16 rows x 64
+K-bytes each, in matrix-core operand order.
 """
 
 from __future__ import annotations
@@ -11,8 +15,12 @@ import torch
 from . import _lib
 
 __all__ = [
+    "pack_weight",
+    "packed_shape",
     "quantize_act_per_token",
     "quantize_weight_per_channel",
+    "unpack_weight",
+    "w8a8_gemm",
     "w8a8_linear",
     "w8a16_linear",
 ]
@@ -45,8 +53,45 @@ def _rows(x: torch.Tensor, k: int) -> torch.Tensor:
     return x2
 
 
+# ---- packed weights --------------------------------------------------------------------------
+
+
+def packed_shape(n: int, k: int) -> tuple[int, int, int]:
+    return ((n + 15) // 16, (k + 63) // 64, 1024)
+
+
+def pack_weight(q: torch.Tensor) -> torch.Tensor:
+    """Row-major (N, K) int8 → packed (ceil(N/16), ceil(K/64), 1024) int8, on the GPU."""
+    _require(q.dim() == 2 and q.dtype == torch.int8, "q must be a 2-D int8 tensor")
+    dev = _on_gpu(q)
+    n, k = q.shape
+    q = q.contiguous()
+    qp = torch.empty(packed_shape(n, k), dtype=torch.int8, device=dev)
+    _lib.check(_lib.library().lse_pack_weight(q.data_ptr(), n, k, qp.data_ptr(), _stream(dev)),
+               "lse_pack_weight")
+    return qp
+
+
+def unpack_weight(qp: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """Inverse of `pack_weight` (a pure permutation, done with torch views): (N, K) int8."""
+    rb, steps, _ = qp.shape
+    t = qp.reshape(rb, steps, 4, 16, 16)  # [rb][step][g = lane // 16][row = lane % 16][16 bytes]
+    t = t.permute(0, 3, 1, 2, 4).reshape(rb * 16, steps * 64)
+    return t[:n, :k].contiguous()
+
+
+def _check_packed(qp: torch.Tensor, n: int, k: int) -> None:
+    _require(qp.dtype == torch.int8 and qp.is_contiguous(), "packed weight must be contiguous int8")
+    _require(tuple(qp.shape) == packed_shape(n, k),
+             f"packed weight has shape {tuple(qp.shape)}, (N, K) = ({n}, {k}) needs "
+             f"{packed_shape(n, k)}")
+
+
+# ---- ops -------------------------------------------------------------------------------------
+
+
 def quantize_weight_per_channel(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """W (N, K) → (q (N, K) int8, s (N,) fp32), s = amax/127 per row, q = clamp(rne(W/s)).
+    """W (N, K) → (q (N, K) int8 row-major, s (N,) fp32), s = amax/127 per row, q = clamp(rne(W/s)).
 
     Runs on the GPU at load time. W is read as fp32 (bf16/fp16 weights widen exactly).
     """
@@ -68,23 +113,24 @@ def quantize_weight_per_channel(w: torch.Tensor) -> tuple[torch.Tensor, torch.Te
 
 def w8a16_linear(
     x: torch.Tensor,
-    qweight: torch.Tensor,
+    qp: torch.Tensor,
     scales: torch.Tensor,
     algo: int = _lib.ALGO_AUTO,
 ) -> torch.Tensor:
-    """y = bf16(s[n] * sum_k x[..., k] q[n, k]) for x (..., K) bf16 → y (..., N) bf16."""
-    n, k = qweight.shape
-    dev = _on_gpu(x, qweight, scales)
+    """y = bf16(s[n] * sum_k x[..., k] q[n, k]) for x (..., K) bf16 → y (..., N) bf16, with the
+    weight q given packed (`pack_weight`)."""
+    dev = _on_gpu(x, qp, scales)
     _require(x.dtype == torch.bfloat16, f"W8A16 expects bf16 activations, got {x.dtype}")
-    _require(qweight.dtype == torch.int8 and qweight.is_contiguous(), "qweight must be contiguous int8")
-    _require(scales.dtype == torch.float32 and scales.shape == (n,), "scales must be fp32 (N,)")
+    _require(scales.dtype == torch.float32 and scales.dim() == 1, "scales must be fp32 (N,)")
+    n, k = scales.shape[0], x.shape[-1]
+    _check_packed(qp, n, k)
     x2 = _rows(x, k)
     m = x2.shape[0]
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     ldx = x2.stride(0) if m > 1 else k
     _lib.check(
         _lib.library().lse_w8a16_gemm_algo(
-            x2.data_ptr(), ldx, qweight.data_ptr(), scales.data_ptr(), y.data_ptr(), n,
+            x2.data_ptr(), ldx, qp.data_ptr(), scales.data_ptr(), y.data_ptr(), n,
             m, n, k, algo, _stream(dev),
         ),
         "lse_w8a16_gemm",
@@ -114,24 +160,26 @@ def quantize_act_per_token(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]
 def w8a8_gemm(
     xq: torch.Tensor,
     sx: torch.Tensor,
-    qweight: torch.Tensor,
+    qp: torch.Tensor,
     scales: torch.Tensor,
     want_acc: bool = False,
     want_y: bool = True,
 ) -> tuple[torch.Tensor | None, torch.Tensor | None]:
-    """(y (M, N) bf16 or None, acc (M, N) int32 or None) from quantized operands."""
-    n, k = qweight.shape
-    dev = _on_gpu(xq, sx, qweight, scales)
-    m = xq.shape[0]
-    _require(xq.dtype == torch.int8 and xq.shape == (m, k) and xq.is_contiguous(), "xq must be (M, K) int8")
+    """(y (M, N) bf16 or None, acc (M, N) int32 or None) from quantized operands; the weight q
+    is given packed."""
+    dev = _on_gpu(xq, sx, qp, scales)
+    _require(scales.dtype == torch.float32 and scales.dim() == 1, "scales must be fp32 (N,)")
+    n = scales.shape[0]
+    _require(xq.dim() == 2, "xq must be (M, K) int8")
+    m, k = xq.shape
+    _require(xq.dtype == torch.int8 and xq.is_contiguous(), "xq must be (M, K) int8")
     _require(sx.dtype == torch.float32 and sx.shape == (m,), "sx must be fp32 (M,)")
-    _require(qweight.dtype == torch.int8 and qweight.is_contiguous(), "qweight must be contiguous int8")
-    _require(scales.dtype == torch.float32 and scales.shape == (n,), "scales must be fp32 (N,)")
+    _check_packed(qp, n, k)
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev) if want_y else None
     acc = torch.empty((m, n), dtype=torch.int32, device=dev) if want_acc else None
     _lib.check(
         _lib.library().lse_w8a8_gemm(
-            xq.data_ptr(), sx.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
+            xq.data_ptr(), sx.data_ptr(), qp.data_ptr(), scales.data_ptr(),
             y.data_ptr() if y is not None else None, n,
             acc.data_ptr() if acc is not None else None, m, n, k, _stream(dev),
         ),
@@ -140,10 +188,10 @@ def w8a8_gemm(
     return y, acc
 
 
-def w8a8_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+def w8a8_linear(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     """Dynamic per-token W8A8: quantize x per row, int8 GEMM with exact int32 accumulation,
     y = bf16((acc * sx[m]) * s[n]). x (..., K) bf16 → y (..., N) bf16."""
-    n = qweight.shape[0]
+    n = scales.shape[0]
     xq, sx = quantize_act_per_token(x)
-    y, _ = w8a8_gemm(xq, sx, qweight, scales)
+    y, _ = w8a8_gemm(xq, sx, qp, scales)
     return y.view(*x.shape[:-1], n)

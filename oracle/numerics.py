@@ -72,6 +72,23 @@ def quantize_weight_per_channel(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return q, s
 
 
+def pack_weight(q: np.ndarray) -> np.ndarray:
+    """Row-major (N, K) int8 → the kernels' packed tile layout, (ceil(N/16), ceil(K/64), 1024).
+
+    Tile (rb, j) byte 16*l + i holds q[16*rb + l % 16, 64*j + 16*(l // 16) + i], zero past N and
+    K. This is a storage permutation, not arithmetic; the layout is this build's own (the
+    reference stores row-major `nn.Linear.weight`, torch/nn/modules/linear.py:53).
+    """
+    q = np.asarray(q, dtype=np.int8)
+    n, k = q.shape
+    nrb, steps = -(-n // 16), -(-k // 64)
+    padded = np.zeros((nrb * 16, steps * 64), np.int8)
+    padded[:n, :k] = q
+    # [rb][row r][step j][group g][byte i] -> [rb][j][g][r][i]
+    t = padded.reshape(nrb, 16, steps, 4, 16).transpose(0, 2, 3, 1, 4)
+    return np.ascontiguousarray(t).reshape(nrb, steps, 1024)
+
+
 def quantize_act_per_token(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """x (M,K) bf16 bits → xq (M,K) int8, sx (M,) float32, the same rule as the weights but per
     row of activations: sx[m] = fl32(max_k |x[m,k]| / 127), xq = clamp(rne(fl32(x / sx))).

@@ -25,7 +25,8 @@ def _declared_functions() -> set[str]:
 def test_header_declares_the_entry_points():
     names = _declared_functions()
     assert {
-        "lse_quantize_weight_per_channel", "lse_w8a16_gemm", "lse_w8a16_gemm_algo",
+        "lse_quantize_weight_per_channel", "lse_packed_weight_bytes", "lse_pack_weight",
+        "lse_w8a16_gemm", "lse_w8a16_gemm_algo",
         "lse_quantize_act_per_token", "lse_w8a8_gemm", "lse_query", "lse_status_string",
     } <= names
 
@@ -65,7 +66,7 @@ E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO = -1, -2, -3, -4, -5
 @pytest.mark.parametrize(
     "args,status",
     [
-        # (x, ldx, q, s, y, ldy, M, N, K, algo)
+        # (x, ldx, qp, s, y, ldy, M, N, K, algo)
         ((FAKE, 64, FAKE, FAKE, FAKE, 64, 1, 64, 60, 0), E_ALIGN),  # K % 16
         ((FAKE, 64, FAKE, FAKE, FAKE, 64, -1, 64, 64, 0), E_SHAPE),
         ((FAKE, 64, None, FAKE, FAKE, 64, 1, 64, 64, 0), E_NULL),
@@ -74,13 +75,17 @@ E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO = -1, -2, -3, -4, -5
         ((None, 64, FAKE, FAKE, FAKE, 64, 1, 64, 64, 0), E_NULL),
         ((FAKE, 60, FAKE, FAKE, FAKE, 64, 2, 64, 64, 0), E_SHAPE),  # ldx < K
         ((FAKE, 68, FAKE, FAKE, FAKE, 64, 2, 64, 64, 0), E_ALIGN),  # ldx % 8
-        ((FAKE, 64, FAKE, FAKE, ctypes.c_void_p((1 << 20) + 1), 64, 2, 64, 64, 0), E_ALIGN),
+        ((FAKE, 64, FAKE, FAKE, ctypes.c_void_p((1 << 20) + 1), 64, 2, 64, 64, 0),
+         E_ALIGN),
         ((FAKE, 64, FAKE, FAKE, FAKE, 32, 2, 64, 64, 0), E_SHAPE),  # ldy < N
-        ((ctypes.c_void_p((1 << 20) + 8), 64, FAKE, FAKE, FAKE, 64, 1, 64, 64, 0), E_ALIGN),
-        ((FAKE, 64, ctypes.c_void_p((1 << 20) + 4), FAKE, FAKE, 64, 1, 64, 64, 0), E_ALIGN),
-        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 65, 64, 64, 1), E_ALGO),  # decode takes M <= 64
+        ((ctypes.c_void_p((1 << 20) + 8), 64, FAKE, FAKE, FAKE, 64, 1, 64, 64, 0),
+         E_ALIGN),
+        ((FAKE, 64, ctypes.c_void_p((1 << 20) + 4), FAKE, FAKE, 64, 1, 64, 64, 0),
+         E_ALIGN),
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 65, 64, 64, 1), E_ALGO),  # decode M <= 64
         ((FAKE, 64, FAKE, FAKE, FAKE, 64, 1, 64, 64, 7), E_ALGO),
         ((FAKE, 1 << 20, FAKE, FAKE, FAKE, 64, 1, 64, 200_000, 0), E_RANGE),
+        ((FAKE, 4096, FAKE, FAKE, FAKE, 1 << 20, 1, 1 << 20, 4096, 0), E_RANGE),
     ],
 )
 def test_w8a16_rejects_bad_arguments(pkg, args, status):
@@ -96,6 +101,18 @@ def test_empty_shapes_are_no_ops(pkg):
     assert lib.lse_w8a8_gemm(None, None, FAKE, FAKE, None, 0, None, 0, 64, 16, None) == 0
     assert lib.lse_quantize_act_per_token(None, 0, None, FAKE, 0, 16, None) == 0
     assert lib.lse_quantize_weight_per_channel(None, 0, None, FAKE, 0, 16, None) == 0
+    assert lib.lse_pack_weight(None, 0, 16, None, None) == 0
+
+
+def test_packed_sizes_and_pack_rejections(pkg):
+    lib = pkg.library()
+    assert lib.lse_packed_weight_bytes(4096, 4096) == 256 * 64 * 1024
+    assert lib.lse_packed_weight_bytes(17, 80) == 2 * 2 * 1024
+    assert lib.lse_packed_weight_bytes(-1, 16) == -1
+    assert lib.lse_pack_weight(FAKE, 16, 40, FAKE, None) == E_ALIGN
+    assert lib.lse_pack_weight(None, 16, 32, FAKE, None) == E_NULL
+    assert lib.lse_pack_weight(FAKE, 16, 32, ctypes.c_void_p((1 << 20) + 8), None) == E_ALIGN
+    assert lib.lse_pack_weight(FAKE, 1 << 20, 4096, FAKE, None) == E_RANGE
 
 
 def test_quantizers_and_w8a8_reject_bad_arguments(pkg):

@@ -31,7 +31,8 @@ def test_forward_matches_oracle(pkg, dev, mode, shape):
     y = mod(x)
     assert y.shape == (*shape[:-1], 192) and y.dtype == torch.bfloat16
     q_ref, s_ref = ora.quantize_weight_per_channel(lin.weight.detach().float().cpu().numpy())
-    np.testing.assert_array_equal(mod.qweight.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(mod.unpacked_qweight().cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(mod.qweight.cpu().numpy(), ora.pack_weight(q_ref))
     np.testing.assert_array_equal(mod.scales.cpu().numpy(), s_ref)
     x_bits = bf16_bits(x.reshape(-1, 256))
     if mode == "int8":

@@ -25,7 +25,7 @@ def _run(pkg, dev, x_bits, q, s, algo, ldy_pad=0):
     m, k = x_bits.shape
     n = q.shape[0]
     x = to_bf16_tensor(x_bits, dev)
-    qt = torch.from_numpy(q).to(dev)
+    qt = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
     st = torch.from_numpy(s).to(dev)
     if ldy_pad:
         sentinel = torch.full((m, n + ldy_pad), -7.0, dtype=torch.bfloat16, device=dev)
@@ -58,9 +58,28 @@ def test_config0_gemv(pkg, dev):
     _check(pkg, dev, 1, 2048, 2048, 0, DECODE)
 
 
+def test_pack_weight_bit_exact(pkg, dev):
+    """The GPU packer against the oracle's layout, with padding past N and K."""
+    rng = np.random.default_rng(3)
+    for n, k in ((1, 16), (37, 80), (272, 1024), (4096, 14336 + 48)):
+        q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+        qp = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(qp.cpu().numpy(), ora.pack_weight(q), err_msg=f"{n}x{k}")
+        np.testing.assert_array_equal(pkg.ops.unpack_weight(qp, n, k).cpu().numpy(), q)
+
+
 @pytest.mark.parametrize("m", [1, 2, 7, 8, 15, 16, 17, 31, 32, 33, 48, 63, 64])
 def test_decode_all_m_tiles(pkg, dev, m):
     _check(pkg, dev, m, 272, 1024, 100 + m, DECODE)
+
+
+@pytest.mark.parametrize("m", [1, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("n,k", [(48, 4096), (4096, 128), (144, 3136), (1000, 1040), (16, 14336)])
+def test_decode_split_panels(pkg, dev, m, n, k):
+    """Few panels with a long K, many panels with a short K, a K tail past the last whole unit,
+    and activations both staged whole and streamed through the LDS ring."""
+    _check(pkg, dev, m, n, k, 11 * m + n + k, DECODE)
 
 
 @pytest.mark.parametrize(
@@ -121,30 +140,27 @@ def test_output_stride_guard_band(pkg, dev, algo):
     assert ora.within_tolerance(y, ora.w8a16_golden(x_bits, q, s))[0]
 
 
-@pytest.mark.parametrize("k", [4096, 14336])
-def test_decode_rows_are_batch_invariant(pkg, dev, k):
+@pytest.mark.parametrize("k,n", [(4096, 512), (14336, 4096), (1024, 6144)])
+def test_decode_rows_are_batch_invariant(pkg, dev, k, n):
     """A row's result does not depend on M or on the other rows within a token class (M <= 16,
-    16 < M <= 64): the graphed decode runs a padded power-of-two bucket while eager decode runs
-    the exact batch, and bucket(M) <= 16 exactly when M <= 16, so both land in one class and
-    must agree bitwise. Across the class boundary rows agree to the tolerance."""
-    x_bits, w = ora.seeded_inputs(31, 64, 512, k)
+    17..32, 33..64): the graphed decode runs a padded power-of-two bucket while eager decode runs
+    the exact batch, and a bucket lies in the same class as the batch it pads, so both must agree
+    bitwise. Across class boundaries rows agree to the tolerance."""
+    x_bits, w = ora.seeded_inputs(31, 64, n, k)
     q, s = ora.quantize_weight_per_channel(w)
-    full = _run(pkg, dev, x_bits, q, s, DECODE)
-    small = _run(pkg, dev, x_bits[:16], q, s, DECODE)
-    for m in (1, 3, 8, 15):
+    top = {16: _run(pkg, dev, x_bits[:16], q, s, DECODE),
+           32: _run(pkg, dev, x_bits[:32], q, s, DECODE),
+           64: _run(pkg, dev, x_bits, q, s, DECODE)}
+    for m, cls in ((1, 16), (3, 16), (8, 16), (15, 16), (17, 32), (31, 32), (33, 64), (63, 64)):
         part = _run(pkg, dev, x_bits[:m], q, s, DECODE)
-        np.testing.assert_array_equal(part, small[:m], err_msg=f"M={m}")
-    for m in (17, 32, 37, 63):
-        part = _run(pkg, dev, x_bits[:m], q, s, DECODE)
-        np.testing.assert_array_equal(part, full[:m], err_msg=f"M={m}")
-    padded = x_bits.copy()
-    padded[40:] = 0
-    np.testing.assert_array_equal(_run(pkg, dev, padded, q, s, DECODE)[:40], full[:40])
-    padded16 = x_bits[:16].copy()
-    padded16[5:] = 0
-    np.testing.assert_array_equal(_run(pkg, dev, padded16, q, s, DECODE)[:5], small[:5])
+        np.testing.assert_array_equal(part, top[cls][:m], err_msg=f"M={m}")
+    for m, cls in ((40, 64), (5, 16), (20, 32)):
+        padded = x_bits[:cls].copy()
+        padded[m:] = 0
+        np.testing.assert_array_equal(_run(pkg, dev, padded, q, s, DECODE)[:m], top[cls][:m])
     golden = ora.w8a16_golden(x_bits[:16], q, s)
-    assert ora.within_tolerance(full[:16], golden)[0] and ora.within_tolerance(small, golden)[0]
+    for cls in (16, 32, 64):
+        assert ora.within_tolerance(top[cls][:16], golden)[0]
 
 
 def test_prefill_rows_are_batch_invariant(pkg, dev):
@@ -176,9 +192,10 @@ def test_llama_decode_shapes_full_size(pkg, dev, k, n):
     gen = torch.Generator(device="cpu").manual_seed(1000 + k + n)
     w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
     q, s = pkg.ops.quantize_weight_per_channel(w)
+    qp = pkg.ops.pack_weight(q)
     for m in (1, 8, 32, 64):
         x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
-        y = pkg.ops.w8a16_linear(x, q, s, algo=DECODE)
+        y = pkg.ops.w8a16_linear(x, qp, s, algo=DECODE)
         ref = _torch_fp32_reference(x, q, s).double().cpu().numpy()
         ok, msg = ora.within_tolerance(bf16_bits(y), ref)
         assert ok, f"M={m} K={k} N={n}: {msg}"
@@ -190,9 +207,10 @@ def test_llama_prefill_shapes_full_size(pkg, dev, k, n):
     gen = torch.Generator(device="cpu").manual_seed(2000 + k + n)
     w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
     q, s = pkg.ops.quantize_weight_per_channel(w)
+    qp = pkg.ops.pack_weight(q)
     for m in (512, 2048):
         x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
-        y = pkg.ops.w8a16_linear(x, q, s, algo=PREFILL)
+        y = pkg.ops.w8a16_linear(x, qp, s, algo=PREFILL)
         ref = _torch_fp32_reference(x, q, s).double().cpu().numpy()
         ok, msg = ora.within_tolerance(bf16_bits(y), ref)
         assert ok, f"M={m} K={k} N={n}: {msg}"

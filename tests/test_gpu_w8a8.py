@@ -18,7 +18,8 @@ LLAMA_SHAPES = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]  # (K,
 def _w8a8(pkg, dev, x_bits, q, s):
     x = to_bf16_tensor(x_bits, dev)
     xq, sx = pkg.ops.quantize_act_per_token(x)
-    y, acc = pkg.ops.w8a8_gemm(xq, sx, torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), True)
+    qp = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
+    y, acc = pkg.ops.w8a8_gemm(xq, sx, qp, torch.from_numpy(s).to(dev), True)
     torch.cuda.synchronize()
     return xq.cpu().numpy(), sx.cpu().numpy(), acc.cpu().numpy(), bf16_bits(y)
 
@@ -38,6 +39,14 @@ def _check(pkg, dev, m, n, k, seed):
 @pytest.mark.parametrize("m", [1, 2, 16, 17, 32, 33, 64])
 def test_decode_kernel_bit_exact(pkg, dev, m):
     _check(pkg, dev, m, 208, 1024, 500 + m)
+
+
+@pytest.mark.parametrize("m", [1, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("n,k", [(48, 4096), (4096, 128), (144, 3136), (16, 14336)])
+def test_decode_split_panels_bit_exact(pkg, dev, m, n, k):
+    """Few panels with a long K and many panels with a short K, staged and streamed
+    activations: the int32 sums stay exact."""
+    _check(pkg, dev, m, n, k, 7 * m + n + k)
 
 
 @pytest.mark.parametrize("m", [65, 128, 200, 512])
@@ -62,10 +71,11 @@ def test_extreme_operands_accumulate_exactly(pkg, dev):
     q[::3] = -127
     sx = np.ones(70, np.float32)
     s = np.ones(n, np.float32)
+    qp = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
     for m in (5, 70):
         y, acc = pkg.ops.w8a8_gemm(
             torch.from_numpy(xq[:m].copy()).to(dev), torch.from_numpy(sx[:m].copy()).to(dev),
-            torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), True,
+            qp, torch.from_numpy(s).to(dev), True,
         )
         torch.cuda.synchronize()
         np.testing.assert_array_equal(acc.cpu().numpy(), ora.w8a8_accumulate(xq[:m], q))
@@ -78,9 +88,10 @@ def test_llama_shapes_full_size(pkg, dev, k, n):
     torch.backends.cuda.matmul.allow_tf32 = False
     x_bits, w = ora.seeded_inputs(3000 + k + n, 512, n, k, outliers=True)
     q, s = pkg.ops.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    qp = pkg.ops.pack_weight(q)
     for m in (1, 32, 512):
         xq, sx = pkg.ops.quantize_act_per_token(to_bf16_tensor(x_bits[:m], dev))
-        y, acc = pkg.ops.w8a8_gemm(xq, sx, q, s, True)
+        y, acc = pkg.ops.w8a8_gemm(xq, sx, qp, s, True)
         exact = (xq.double() @ q.double().t()).round().to(torch.int64)
         assert torch.equal(acc.to(torch.int64), exact), f"M={m} K={k} N={n}"
         y_ref = ora.w8a8_epilogue(acc.cpu().numpy(), sx.cpu().numpy(), s.cpu().numpy())
@@ -91,7 +102,7 @@ def test_acc_only_and_y_only(pkg, dev):
     x_bits, w = ora.seeded_inputs(61, 20, 64, 256, outliers=True)
     q, s = ora.quantize_weight_per_channel(w)
     xq, sx = pkg.ops.quantize_act_per_token(to_bf16_tensor(x_bits, dev))
-    qt, st = torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)
+    qt, st = pkg.ops.pack_weight(torch.from_numpy(q).to(dev)), torch.from_numpy(s).to(dev)
     y_only, none_acc = pkg.ops.w8a8_gemm(xq, sx, qt, st, want_acc=False, want_y=True)
     none_y, acc_only = pkg.ops.w8a8_gemm(xq, sx, qt, st, want_acc=True, want_y=False)
     assert none_acc is None and none_y is None

@@ -35,7 +35,7 @@ def test_int8_linear_holds_buffers_not_parameters(pkg):
     mod = pkg.Int8Linear(64, 32, mode="w8a8", bias=True)
     assert list(mod.parameters()) == []
     names = dict(mod.named_buffers())
-    assert names["qweight"].dtype == torch.int8 and names["qweight"].shape == (32, 64)
+    assert names["qweight"].dtype == torch.int8 and names["qweight"].shape == (2, 1, 1024)
     assert names["scales"].dtype == torch.float32 and names["scales"].shape == (32,)
     assert names["bias"].dtype == torch.bfloat16
     assert "mode=w8a8" in repr(mod)
@@ -86,3 +86,17 @@ def test_ops_refuse_wrong_dtypes_before_touching_the_device(pkg):
     s = torch.ones(16)
     with pytest.raises(RuntimeError, match="CUDA"):
         pkg.ops.w8a16_linear(x, q, s)
+
+
+def test_unpack_inverts_the_oracle_packing(pkg):
+    """The module's host-side unpack (torch views) against the oracle's packing, with padding."""
+    import numpy as np
+
+    from oracle import numerics as ora
+
+    rng = np.random.default_rng(4)
+    for n, k in ((1, 16), (37, 80), (64, 256)):
+        q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+        qp = torch.from_numpy(ora.pack_weight(q))
+        assert tuple(qp.shape) == pkg.ops.packed_shape(n, k)
+        np.testing.assert_array_equal(pkg.ops.unpack_weight(qp, n, k).numpy(), q)

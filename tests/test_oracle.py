@@ -281,3 +281,42 @@ def test_config0_digests():
         for name, a in (("x_bits", x_bits), ("q", q), ("s", s), ("y_bits", y))
     }
     assert got == digests
+
+
+# ---- packed weight layout ------------------------------------------------------------------
+
+
+def test_pack_weight_matches_the_layout_definition_by_brute_force():
+    """Every byte of every tile, walked with explicit loops from the layout's definition,
+    including the zero padding past N and K (N=37, K=80: three row tiles, two K steps)."""
+    rng = np.random.default_rng(17)
+    q = rng.integers(-127, 128, (37, 80)).astype(np.int8)
+    qp = ora.pack_weight(q)
+    assert qp.shape == (3, 2, 1024) and qp.dtype == np.int8
+    for rb in range(3):
+        for j in range(2):
+            for lane in range(64):
+                for i in range(16):
+                    row, col = 16 * rb + lane % 16, 64 * j + 16 * (lane // 16) + i
+                    expect = q[row, col] if row < 37 and col < 80 else 0
+                    assert qp[rb, j, 16 * lane + i] == expect, (rb, j, lane, i)
+
+
+def test_pack_weight_feeds_the_tile_walk_that_the_kernels_do():
+    """A dot product computed the way the kernels consume tiles (lane l of tile (rb, j) holds 16
+    K-consecutive weights of row l % 16 starting at 64 j + 16 (l // 16)) reproduces x·qᵀ
+    exactly; a transposed or shifted layout would not."""
+    rng = np.random.default_rng(18)
+    n, k = 48, 192
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    x = rng.integers(-5, 6, (3, k)).astype(np.int64)
+    qp = ora.pack_weight(q)
+    y = np.zeros((3, n), np.int64)
+    for rb in range(qp.shape[0]):
+        for j in range(qp.shape[1]):
+            tile = qp[rb, j].reshape(64, 16).astype(np.int64)
+            for lane in range(64):
+                row = 16 * rb + lane % 16
+                k0 = 64 * j + 16 * (lane // 16)
+                y[:, row] += x[:, k0:k0 + 16] @ tile[lane]
+    np.testing.assert_array_equal(y, x @ q.astype(np.int64).T)
