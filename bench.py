@@ -91,13 +91,18 @@ def bench_decode(pkg, dev, steps: int, warmup: int, gen) -> dict:
             for m in DECODE_MS for _, n in SHAPES}
     # Raw C-ABI launches (m, k, n, args without the stream), replayed from a captured graph so
     # the timed region measures the kernels, not host-side launch cost.
+    # The launches run in order on one stream, so they share one workspace of the largest size.
+    lib = pkg.library()
+    ws_bytes = max(lib.lse_workspace_bytes(0, m, n, k) for m in DECODE_MS for k, n in SHAPES)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     calls = []
     for m in DECODE_MS:
         for layer in range(LAYERS):
             for si, (k, n) in enumerate(SHAPES):
                 q, s = weights[si][layer]
                 calls.append((m, k, n, (xs[(m, k)].data_ptr(), k, q.data_ptr(), s.data_ptr(),
-                                        outs[(m, n)].data_ptr(), n, m, n, k, 1)))
+                                        outs[(m, n)].data_ptr(), n, m, n, k, 1, ws.data_ptr(),
+                                        ws_bytes)))
     fn_ptr = pkg.library().lse_w8a16_gemm_algo
 
     def graph_of(sub):

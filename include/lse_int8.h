@@ -12,7 +12,10 @@
  *
  * Conventions shared by every entry point:
  *  - All pointers are device pointers. The caller owns every buffer; the library keeps no state
- *    beyond its compiled kernels and allocates nothing.
+ *    beyond its compiled kernels and allocates nothing. The decode GEMMs of some shapes add
+ *    partial sums of K ranges in a second pass through a caller-provided workspace of
+ *    lse_workspace_bytes(...) bytes (0 for most calls); a workspace may be reused by calls that
+ *    are ordered on one stream, never by calls that can overlap.
  *  - Weights travel in the packed tile layout written by lse_pack_weight: tiles of 16 rows x 64
  *    K-bytes, 1 KB each, tile (rb, j) at byte (rb * ceil(K/64) + j) * 1024, its byte 16*l + i
  *    holding q[16*rb + l%16][64*j + 16*(l/16) + i], zero past N and K. One 128-bit load per lane
@@ -48,6 +51,13 @@ enum lse_status {
   LSE_E_ALIGN = -3,       /* K, a stride or a pointer misses the alignment the kernels load with */
   LSE_E_RANGE = -4,       /* K too large for exact int32 accumulation, or a size beyond int32 grids */
   LSE_E_ALGO = -5,        /* unknown algorithm id, or one that cannot run this shape */
+  LSE_E_WORKSPACE = -6,   /* workspace NULL or smaller than lse_workspace_bytes for the call */
+};
+
+/* Arithmetic mode, for lse_workspace_bytes. */
+enum lse_mode {
+  LSE_MODE_W8A16 = 0,
+  LSE_MODE_W8A8 = 1,
 };
 
 /* Algorithm selector for lse_w8a16_gemm_algo. */
@@ -66,7 +76,7 @@ enum lse_query_key {
   LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
 };
 
-#define LSE_ABI_VERSION 2
+#define LSE_ABI_VERSION 3
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -95,21 +105,33 @@ int64_t lse_packed_weight_bytes(int64_t N, int64_t K);
 int lse_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, void* stream);
 
 /*
+ * Bytes of device workspace (16-byte aligned) that lse_w8a16_gemm (mode LSE_MODE_W8A16) or
+ * lse_w8a8_gemm (LSE_MODE_W8A8) needs for an (M, N, K) call on the current device; 0 when the
+ * call needs none, -1 for a negative size or an unknown mode. At most 64 * M * (N + 15).
+ * Replaces: nothing in the reference; callers size the buffer with it, as cuBLASLt callers do.
+ */
+int64_t lse_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K);
+
+/*
  * W8A16 linear: y[m,n] = bf16_rne(s[n] * sum_k x[m,k] * q[n,k]), fp32 accumulation.
  * x: (M, K) bf16, row stride ldx (multiple of 8, 16-byte aligned base).
  * qp: packed (N, K) int8 weight, K % LSE_K_ALIGN == 0. s: (N) fp32.
  * y: (M, N) bf16, row stride ldy >= N (any; 8-byte stores are used when ldy % 4 == 0 and the
  *    base is 8-byte aligned, 2-byte stores otherwise).
+ * workspace: workspace_bytes >= lse_workspace_bytes(LSE_MODE_W8A16, M, N, K) bytes, 16-byte
+ *    aligned (may be NULL when that is 0).
  * Replaces: `F.linear(x, W)` of `nn.Linear.forward` (torch/nn/modules/linear.py:134) at
  * model_runner.py:322-324, 369, 418 and modeling_llama.py:175 (LlamaMLP.forward).
  */
 int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
-                   int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
+                   int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                   int64_t workspace_bytes, void* stream);
 
 /* lse_w8a16_gemm with the kernel family chosen by the caller (enum lse_algo); used to test
  * the decode and prefill kernels on identical inputs. Same contract otherwise. */
 int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
-                        int64_t ldy, int64_t M, int64_t N, int64_t K, int algo, void* stream);
+                        int64_t ldy, int64_t M, int64_t N, int64_t K, int algo, void* workspace,
+                        int64_t workspace_bytes, void* stream);
 
 /*
  * Dynamic per-token activation quantization (W8A8 first stage).
@@ -128,11 +150,13 @@ int lse_quantize_act_per_token(const void* x, int64_t ldx, int8_t* xq, float* sx
  * xq: (M, K) int8 contiguous; qp: packed (N, K) int8 weight; K % LSE_K_ALIGN == 0,
  * K <= LSE_MAX_K. y: (M, N) bf16 with row stride ldy >= N, or NULL to skip it.
  * acc: (M, N) int32 contiguous, or NULL to skip it (the bit-exact test reads it).
+ * workspace: as for lse_w8a16_gemm, sized by lse_workspace_bytes(LSE_MODE_W8A8, M, N, K).
  * Replaces: `F.linear(x, W)` (torch/nn/modules/linear.py:134) at the same call sites as
  * lse_w8a16_gemm, in the dynamic per-token mode.
  */
 int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* y,
-                  int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream);
+                  int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* workspace,
+                  int64_t workspace_bytes, void* stream);
 
 /* Static properties (enum lse_query_key); -1 for an unknown key. Load-time checks read these,
  * as `ModelRunner.check_custom_kernel_support` (model_runner.py:77-94) checks its kernels. */

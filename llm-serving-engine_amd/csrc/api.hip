@@ -14,12 +14,13 @@ int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, i
                         int64_t K, hipStream_t stream);
 int launch_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, hipStream_t stream);
 int64_t packed_weight_bytes(int64_t N, int64_t K);
+int64_t skinny_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K);
 int launch_w8a16_skinny(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
-                        uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                        hipStream_t stream);
+                        uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                        int64_t ws_bytes, hipStream_t stream);
 int launch_w8a8_skinny(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
                        uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
-                       hipStream_t stream);
+                       void* ws, int64_t ws_bytes, hipStream_t stream);
 int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* q, const float* s, uint16_t* y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s,
@@ -152,8 +153,18 @@ int lse_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, void* str
   return lse::launch_pack_weight(q, N, K, qp, (hipStream_t)stream);
 }
 
+int64_t lse_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0 || (mode != LSE_MODE_W8A16 && mode != LSE_MODE_W8A8)) return -1;
+  // Only the decode kernel uses a workspace; shapes it rejects need none.
+  if (M == 0 || N == 0 || K == 0 || M > LSE_DECODE_MAX_M || N > kMaxRows || K > LSE_MAX_K ||
+      K % LSE_K_ALIGN)
+    return 0;
+  return lse::skinny_workspace_bytes(mode == LSE_MODE_W8A8, M, N, K);
+}
+
 int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
-                        int64_t ldy, int64_t M, int64_t N, int64_t K, int algo, void* stream) {
+                        int64_t ldy, int64_t M, int64_t N, int64_t K, int algo, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
   if (int st = check_common(qp, s, M, N, K)) return st;
   if (algo < LSE_ALGO_AUTO || algo > LSE_ALGO_PREFILL) return LSE_E_ALGO;
   if (algo == LSE_ALGO_DECODE && M > LSE_DECODE_MAX_M) return LSE_E_ALGO;
@@ -167,19 +178,24 @@ int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const floa
   if (algo == LSE_ALGO_DECODE) {
     // The decode kernel addresses x through a 32-bit buffer resource.
     if (((M - 1) * ldx + K) * 2 >= (int64_t)kBufferLimit) return LSE_E_RANGE;
-    return lse::launch_w8a16_skinny((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K, st);
+    if (workspace_bytes < 0 || (workspace && !aligned(workspace, 16))) return LSE_E_WORKSPACE;
+    return lse::launch_w8a16_skinny((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K,
+                                    workspace, workspace_bytes, st);
   }
   if ((M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
   return lse::launch_w8a16_gemm((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K, st);
 }
 
 int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
-                   int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
-  return lse_w8a16_gemm_algo(x, ldx, qp, s, y, ldy, M, N, K, LSE_ALGO_AUTO, stream);
+                   int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+  return lse_w8a16_gemm_algo(x, ldx, qp, s, y, ldy, M, N, K, LSE_ALGO_AUTO, workspace,
+                             workspace_bytes, stream);
 }
 
 int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* y,
-                  int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream) {
+                  int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* workspace,
+                  int64_t workspace_bytes, void* stream) {
   if (int st = check_common(qp, s, M, N, K)) return st;
   if (M == 0 || N == 0) return LSE_OK;
   if (!sx) return LSE_E_NULL;
@@ -201,7 +217,9 @@ int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const flo
   if (int e = check_packed(N, K)) return e;
   if (M <= LSE_DECODE_MAX_M) {
     if (M * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
-    return lse::launch_w8a8_skinny(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, st);
+    if (workspace_bytes < 0 || (workspace && !aligned(workspace, 16))) return LSE_E_WORKSPACE;
+    return lse::launch_w8a8_skinny(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, workspace,
+                                   workspace_bytes, st);
   }
   if ((M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
   return lse::launch_w8a8_gemm(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, st);
@@ -226,6 +244,7 @@ const char* lse_status_string(int status) {
     case LSE_E_ALIGN: return "K, a stride or a pointer is not aligned as the kernels require";
     case LSE_E_RANGE: return "size out of range (int32 accumulation or grid limits)";
     case LSE_E_ALGO: return "unknown algorithm, or one that cannot run this shape";
+    case LSE_E_WORKSPACE: return "workspace missing, misaligned or smaller than lse_workspace_bytes";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
   }
 }

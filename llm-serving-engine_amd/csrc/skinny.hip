@@ -6,14 +6,18 @@
 // (lse_common.h) so that each 128-bit load of a wave is one contiguous 1 KB tile.
 //
 // Work decomposition.
-//  * A panel is RT row tiles (16 * RT weight rows). Each workgroup takes a contiguous range of
-//    whole panels (the panels split as evenly as whole panels allow) and streams them one after
-//    another.
-//  * Within a panel the W waves split the 64-wide K steps round-robin (wave w takes steps w,
-//    w + W, ...; a "unit" is one step of every wave). A wave multiplies each activation fragment
-//    against all RT row tiles of the panel, so activations are read 2M/(16 RT) times per weight
-//    byte. At the end of a panel the waves' partial sums are added through LDS in wave order,
-//    scaled and stored.
+//  * A panel is RT row tiles (16 * RT weight rows). The K steps split into S ranges of `ssteps`
+//    steps; a work unit is (split, panel), numbered split-major. Each workgroup takes a
+//    contiguous range of whole units (split as evenly as whole units allow) and streams them one
+//    after another.
+//  * Within a unit the W waves split the unit's 64-wide K steps round-robin (wave w takes steps
+//    w, w + W, ...; a "super-step" is one step of every wave). A wave multiplies each activation
+//    fragment against all RT row tiles of the panel, so activations are read 2M/(16 RT) times
+//    per weight byte: wide panels keep that traffic (from L2) below the weight stream (from
+//    HBM), and splitting K keeps enough units to fill every CU when panels are wide. At the end
+//    of a unit the waves' partial sums are added through LDS in wave order; with S = 1 they are
+//    scaled and stored, with S > 1 stored raw to a workspace that skinny_reduce adds over the
+//    splits in split order before the same epilogue.
 //  * Every summation order depends only on (N, K, the token class of M, the grid), never on M
 //    inside a class or on other rows: results are deterministic and a row's output is the same
 //    inside any batch of its class. No atomics.
@@ -55,8 +59,45 @@ struct SkinnyArgs {
   int nsteps;           // ceil(K / 64)
   int nrb;              // ceil(N / 16)
   int panels;           // ceil(nrb / RT)
-  int NSU;              // units per panel: ceil(nsteps / W) rounded up to a multiple of DW
+  int splits;           // S, ranges the K steps split into
+  int ssteps;           // steps per range: ceil(nsteps / S)
+  int units;            // panels * splits
+  int NSU;              // super-steps per unit: ceil(ssteps / W) rounded up to a multiple of DW
+  void* part;           // S > 1: raw partial sums [S][M][16 nrb], fp32 (W8A16) or int32 (W8A8)
 };
+
+// The scaled output of one lane: `v` holds rows n..n+3 (cnt of them valid) of token m, `sc` their
+// scales, sxm the token's scale (W8A8). W8A16: y = bf16(v * s[n]); W8A8: acc = v (int32, when
+// requested), y = bf16((v * sx[m]) * s[n]).
+template <bool I8, typename Acc>
+__device__ __forceinline__ void skinny_epilogue(const SkinnyArgs& a, int m, int n, int cnt, Acc v,
+                                                const float (&sc)[4], float sxm, bool yvec) {
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if constexpr (I8)
+      o[r] = ((float)v[r] * sxm) * sc[r];
+    else
+      o[r] = v[r] * sc[r];
+  }
+  if constexpr (I8) {
+    if (a.acc) {
+      int32_t* dst = a.acc + (int64_t)m * a.N + n;
+      if (cnt == 4 && (a.N & 3) == 0) {
+        *reinterpret_cast<i32x4*>(dst) = v;
+      } else {
+        for (int r = 0; r < cnt; ++r) dst[r] = v[r];
+      }
+    }
+    if (!a.y) return;
+  }
+  uint16_t* out = a.y + (int64_t)m * a.ldy + n;
+  if (cnt == 4 && yvec) {
+    *reinterpret_cast<uint2*>(out) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+  } else {
+    for (int r = 0; r < cnt; ++r) out[r] = f32_to_bf16(o[r]);
+  }
+}
 
 // Register stage of the weight ring: one 1 KB tile per row tile of the panel.
 template <int RT>
@@ -91,7 +132,6 @@ skinny_kernel(SkinnyArgs a) {
   // A single accumulator chain in W8A16 splits into two (one per dequantized half), so the two
   // MFMAs of a step do not wait on each other.
   constexpr int NACC = (!I8 && SLICES == 1) ? 2 : 1;
-  static_assert(W % RT == 0, "a wave's epilogue slices share one row tile");
   static_assert(!XLDS || MT == 1, "activations are staged whole for one token tile only");
   static_assert(DW % DX == 0, "the activation ring index must repeat with the weight ring's");
   // Streamed activations: a wave's ring slot holds the 16 MT token rows x 64 K-columns of one of
@@ -129,8 +169,9 @@ skinny_kernel(SkinnyArgs a) {
   const int r16 = lane & 15;
   const int g = lane >> 4;
   const int G = gridDim.x;
-  const int p_first = blockIdx.x * a.panels / G;
-  const int p_end = (blockIdx.x + 1) * a.panels / G;
+  const int u_first = blockIdx.x * a.units / G;
+  const int u_end = (blockIdx.x + 1) * a.units / G;
+  const bool split = a.splits > 1;
 
   const BufferRsrc qres = make_rsrc(a.qp, (uint32_t)a.nrb * (uint32_t)a.nsteps * kTileBytes);
   const BufferRsrc xres = make_rsrc(a.x, (uint32_t)(((int64_t)(a.M - 1) * a.ldx + a.K) * ESZ));
@@ -141,13 +182,13 @@ skinny_kernel(SkinnyArgs a) {
     sxv[b] = (I8 && m < a.M) ? a.sx[m] : 0.0f;
   }
 
-  // Staged inputs, issued before the weight ring: the scales of rows [16 RT p_first, 16 RT p_end)
-  // (through registers), and with XLDS all activations, copied straight to LDS: piece i of the
+  // Staged inputs, issued before the weight ring: with S = 1 (units are panels) the scales of
+  // rows [16 RT u_first, 16 RT u_end) (through registers), and with XLDS all activations, copied straight to LDS: piece i of the
   // image is bytes [1024 i, 1024 i + 1024), lane l fills byte 1024 i + 16 l, which is physical
   // chunk pc of row m and holds logical chunk pc ^ swz(m); tokens past M and K past the end read
   // zeros, so the image needs no bounds checks when read.
-  const int srow0 = 16 * RT * p_first;
-  const int nsc = min(16 * RT * p_end, a.N) - srow0;
+  const int srow0 = 16 * RT * u_first;
+  const int nsc = split ? 0 : min(16 * RT * u_end, a.N) - srow0;
   constexpr int kScPerThread = (kSkinnyScaleLds + 64 * W - 1) / (64 * W);
   float sc_stage[kScPerThread];
 #pragma unroll
@@ -181,11 +222,12 @@ skinny_kernel(SkinnyArgs a) {
     __syncthreads();
   };
 
-  // Weight load cursor: panel lp, unit lsu within it.
-  int lp = p_first, lsu = 0;
+  // Weight load cursor: unit lu (panel lp of split lsp), super-step lsu within it.
+  int lu = u_first, lp = u_first % a.panels, lsp = u_first / a.panels, lsu = 0;
   auto load_w = [&](SkinnyWStage<RT>& st) {
-    const int j = W * lsu + wave;
-    const bool kv = lp < p_end && j < a.nsteps;
+    const int jr = W * lsu + wave;
+    const int j = lsp * a.ssteps + jr;
+    const bool kv = lu < u_end && jr < a.ssteps && j < a.nsteps;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int rb = lp * RT + rt;
@@ -195,17 +237,22 @@ skinny_kernel(SkinnyArgs a) {
     }
     if (++lsu == a.NSU) {
       lsu = 0;
-      ++lp;
+      ++lu;
+      if (++lp == a.panels) {
+        lp = 0;
+        ++lsp;
+      }
     }
   };
   // Activation load cursor (activations depend on the step only, not on the panel). Piece i of
   // this wave's part of a slot covers bytes [1024 i, 1024 i + 1024): lane l fills byte
   // 1024 i + 16 l, physical chunk pc of token row m, which holds logical chunk pc ^ (m % XCH).
   // Tokens past M, K past the end and steps past the range read zeros.
-  int xp = p_first, xsu = 0;
+  int xu = u_first, xp = u_first % a.panels, xsp = u_first / a.panels, xsu = 0;
   auto load_x = [&](int slot) {
-    const int j = W * xsu + wave;
-    const bool live = xp < p_end && j < a.nsteps;
+    const int jr = W * xsu + wave;
+    const int j = xsp * a.ssteps + jr;
+    const bool live = xu < u_end && jr < a.ssteps && j < a.nsteps;
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
       const int o = 1024 * i + 16 * lane;
@@ -221,7 +268,11 @@ skinny_kernel(SkinnyArgs a) {
     }
     if (++xsu == a.NSU) {
       xsu = 0;
-      ++xp;
+      ++xu;
+      if (++xp == a.panels) {
+        xp = 0;
+        ++xsp;
+      }
     }
   };
 
@@ -233,18 +284,20 @@ skinny_kernel(SkinnyArgs a) {
 #pragma unroll
       for (int c = 0; c < NACC; ++c) acc[rt][b][c] = Acc{0, 0, 0, 0};
 
-  // One step: the wave's K step of unit su, from weight stage st and ring slot `slot`.
+  // One step: the wave's K step of super-step su of a unit of split sp, from weight stage st and
+  // ring slot `slot`.
   // XLDS: this lane's token row (tokens past M re-read row M-1; their outputs are dropped).
   const int x_m = min(r16, a.M - 1);
   const unsigned char* x_row_base = x_lds + x_m * xrow_bytes;
   const int x_swz = x_m & xswz;
-  auto compute = [&](const SkinnyWStage<RT>& st, int slot, int su) {
+  auto compute = [&](const SkinnyWStage<RT>& st, int slot, int sp, int su) {
     uint4 xv[MT][XL];
     if constexpr (XLDS) {
-      // A padding step past the last K step (NSU is rounded up to the ring depth) re-reads step
-      // 0; its weights are zero.
-      const int j = W * su + wave;
-      const int c0 = (j < a.nsteps ? j : 0) * 4 * ESZ + XL * g;
+      // A padding step past the unit's range or the last K step (NSU is rounded up to the ring
+      // depth) re-reads step 0; its weights are zero.
+      const int jr = W * su + wave;
+      const int j = sp * a.ssteps + jr;
+      const int c0 = (jr < a.ssteps && j < a.nsteps ? j : 0) * 4 * ESZ + XL * g;
 #pragma unroll
       for (int h = 0; h < XL; ++h)
         xv[0][h] = *reinterpret_cast<const uint4*>(x_row_base + 16 * ((c0 + h) ^ x_swz));
@@ -285,45 +338,32 @@ skinny_kernel(SkinnyArgs a) {
     }
   };
 
-  // Scales and stores one lane's four outputs (rows n..n+3 of token m of panel p's slice).
+  // One lane's four outputs of a unit: rows n..n+3 of token m of slice `slice` of panel p.
+  // S = 1: scaled and stored; S > 1: raw, to split sp's part of the workspace (rows padded to
+  // 16 nrb, so every tile stores whole).
   const bool yvec = a.y && (a.ldy & 3) == 0 && ((uintptr_t)a.y & 7) == 0;
-  auto store_out = [&](int p, int slice, Acc v) {
+  auto store_out = [&](int p, int sp, int slice, Acc v) {
     const int rt = slice % RT, b = slice / RT;
     const int m = 16 * b + r16;
-    const int n = 16 * (p * RT + rt) + 4 * g;
+    const int rb = p * RT + rt;
+    const int n = 16 * rb + 4 * g;
+    if (split) {
+      if (m < a.M && rb < a.nrb)
+        *reinterpret_cast<Acc*>(static_cast<char*>(a.part) +
+                                (((int64_t)sp * a.M + m) * (16 * a.nrb) + n) * 4) = v;
+      return;
+    }
     if (m >= a.M || n >= a.N) return;
     const int cnt = min(4, a.N - n);
-    float o[4];
+    float sc[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float sc = r < cnt ? s_lds[n + r - srow0] : 0.0f;
-      if constexpr (I8)
-        o[r] = ((float)v[r] * sxv[b]) * sc;
-      else
-        o[r] = v[r] * sc;
-    }
-    if constexpr (I8) {
-      if (a.acc) {
-        int32_t* dst = a.acc + (int64_t)m * a.N + n;
-        if (cnt == 4 && (a.N & 3) == 0) {
-          *reinterpret_cast<i32x4*>(dst) = v;
-        } else {
-          for (int r = 0; r < cnt; ++r) dst[r] = v[r];
-        }
-      }
-      if (!a.y) return;
-    }
-    uint16_t* out = a.y + (int64_t)m * a.ldy + n;
-    if (cnt == 4 && yvec) {
-      *reinterpret_cast<uint2*>(out) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
-    } else {
-      for (int r = 0; r < cnt; ++r) out[r] = f32_to_bf16(o[r]);
-    }
+    for (int r = 0; r < 4; ++r) sc[r] = r < cnt ? s_lds[n + r - srow0] : 0.0f;
+    skinny_epilogue<I8>(a, m, n, cnt, v, sc, sxv[b], yvec);
   };
 
-  // End of panel p: pass i adds slices [i W, i W + RSLOTS) over the waves in wave order; wave w
-  // keeps slice i W + w, scales and stores it.
-  auto panel_end = [&](int p) {
+  // End of a unit (panel p of split sp): pass i adds slices [i W, i W + RSLOTS) over the waves in
+  // wave order; wave w keeps slice i W + w and stores it.
+  auto unit_end = [&](int p, int sp) {
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
       __syncthreads();  // the previous pass's (or panel's) reads of red are done
@@ -343,7 +383,7 @@ skinny_kernel(SkinnyArgs a) {
         Acc v = red[0][wave][lane];
 #pragma unroll
         for (int w2 = 1; w2 < W; ++w2) v += red[w2][wave][lane];
-        store_out(p, slice, v);
+        store_out(p, sp, slice, v);
       }
     }
 #pragma unroll
@@ -354,7 +394,7 @@ skinny_kernel(SkinnyArgs a) {
         for (int c = 0; c < NACC; ++c) acc[rt][b][c] = Acc{0, 0, 0, 0};
   };
 
-  if (p_first >= p_end) return;
+  if (u_first >= u_end) return;
   SkinnyWStage<RT> wr[DW];
   // Prologue in the steady state's issue order (weights of step t + DW - 1, then activations of
   // unit t + DX - 1), so the activation wait count is the same at every step.
@@ -367,33 +407,58 @@ skinny_kernel(SkinnyArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
   store_staged();
-  for (int p = p_first; p < p_end; ++p) {
-    // NSU is a multiple of DW, so every panel starts at ring stage 0.
+  for (int u = u_first; u < u_end; ++u) {
+    const int p = u % a.panels, sp = u / a.panels;
+    // NSU is a multiple of DW, so every unit starts at ring stage 0.
     for (int su = 0; su < a.NSU; su += DW) {
 #pragma unroll
       for (int i = 0; i < DW; ++i) {
         load_w(wr[(i + DW - 1) % DW]);
         if constexpr (!XLDS) load_x((i + DX - 1) % DX);
         __builtin_amdgcn_sched_barrier(0);
-        compute(wr[i], i % DX, su + i);
+        compute(wr[i], i % DX, sp, su + i);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    panel_end(p);
+    unit_end(p, sp);
   }
+}
+
+// Second pass of a split launch: y (and acc) from the S raw partial sums of each output, added in
+// split order. One thread per token and group of four rows; the workspace rows are 16 nrb long.
+template <bool I8>
+__global__ void __launch_bounds__(256)
+skinny_reduce(SkinnyArgs a) {
+  using Acc = std::conditional_t<I8, i32x4, f32x4>;
+  const int groups = 4 * a.nrb;  // four-row groups per token
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)a.M * groups) return;
+  const int m = (int)(t / groups);
+  const int n = 4 * (int)(t - (int64_t)m * groups);
+  if (n >= a.N) return;
+  const int64_t split_stride = (int64_t)a.M * 16 * a.nrb;
+  const Acc* src = reinterpret_cast<const Acc*>(static_cast<const char*>(a.part) +
+                                                ((int64_t)m * 16 * a.nrb + n) * 4);
+  Acc v = src[0];
+  for (int sp = 1; sp < a.splits; ++sp) v += src[sp * split_stride / 4];
+  const int cnt = min(4, a.N - n);
+  float sc[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sc[r] = r < cnt ? a.s[n + r] : 0.0f;
+  const bool yvec = a.y && (a.ldy & 3) == 0 && ((uintptr_t)a.y & 7) == 0;
+  skinny_epilogue<I8>(a, m, n, cnt, v, sc, I8 ? a.sx[m] : 0.0f, yvec);
 }
 
 // ---- host side -----------------------------------------------------------------------------
 
 // Kernel configuration: token tiles MT (the class of M), row tiles per panel RT, waves W, ring
-// depths. W, RT and MT fix every summation order, so they depend on the class and on N only,
-// never on M inside a class. Panels of 64 rows (RT = 4) when there are enough of them to fill the
-// CUs, 32 rows when there are half as many, else single row tiles; larger panels read the
-// activations fewer times per weight byte. Staged (XLDS) and streamed activations feed the same
-// MFMAs in the same order, so the choice between them (by M and K) changes no result.
+// depths, K splits S. MT, RT, W and S fix every summation order, so they depend on the class, N,
+// K and the CU count only, never on M inside a class. Staged (XLDS) and streamed activations feed
+// the same MFMAs in the same order, so the choice between them (by M and K) changes no result.
 struct SkinnyShape {
   int mt, rt, w, dw;
   bool xlds;
+  int splits;
 };
 
 template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS>
@@ -401,20 +466,33 @@ static const void* skinny_fn() {
   return reinterpret_cast<const void*>(&skinny_kernel<I8, MT, RT, W, DW, DX, XLDS>);
 }
 
+// Panel height for 17..64 tokens: each panel re-reads the activations from L2, so panels are as
+// tall as the row-tile count allows while still giving every CU work (measured on MI355X: 64-row
+// panels from 1024 row tiles up, 32-row panels from 384).
 static int skinny_rt(int64_t N) {
   const int64_t nrb = ceil_div(N, kTileRows);
   return nrb >= 1024 ? 4 : nrb >= 384 ? 2 : 1;
+}
+
+// Few row tiles and a deep K (the MLP down projection): one panel per CU would read all of the
+// activations once per 16 rows. Four K splits of 64-row panels cut that traffic fourfold, and
+// the partial sums (4 x M x N fp32) stay small next to the weights, so the second pass that adds
+// them is cheap. Wider N would make the partial sums, and that pass, too large to pay off.
+static bool skinny_split_k(int64_t N, int64_t K) {
+  return ceil_div(N, kTileRows) <= 256 && ceil_div(K, kTileK) >= 128;
 }
 
 template <bool I8>
 static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K) {
   if (M <= 16) {
     const bool fits = M * (size_t)skinny_x_row((int)K, I8 ? 1 : 2) <= (size_t)kSkinnyXLdsBytes;
-    return {1, 1, 8, 4, fits};
+    return {1, 1, 8, 4, fits, 1};
   }
+  const int mt = M <= 32 ? 2 : 4;
+  if (skinny_split_k(N, K)) return {mt, 4, 4, 4, false, 4};
   const int rt = skinny_rt(N);
-  if (M <= 32) return {2, rt, rt == 4 ? 4 : 8, 4, false};
-  return {4, rt, 4, 4, false};
+  if (mt == 2) return {2, rt, rt == 4 ? 4 : 8, 4, false, 1};
+  return {4, rt, 4, 4, false, 1};
 }
 
 template <bool I8>
@@ -435,25 +513,28 @@ static const void* skinny_kernel_for(const SkinnyShape& sh) {
 struct SkinnyPlan {
   SkinnyShape sh;
   const void* fn;
-  SkinnyArgs a;  // shape fields only
+  SkinnyArgs a;       // shape fields only
   int grid;
   size_t x_lds;
+  int64_t part_bytes;  // workspace for the raw partial sums (0 when S = 1)
 };
 
-// Whole panels per workgroup, spread as evenly as whole panels allow over the resident
-// workgroups; the scales of a workgroup's panels must fit its LDS array.
-static int skinny_grid(int panels, int rt, int resident) {
-  const int kmax = kSkinnyScaleLds / (16 * rt);
-  const int per = (int)std::min<int64_t>(ceil_div(panels, resident), kmax);
-  return (int)ceil_div(panels, per);
+// Whole units per workgroup, spread as evenly as whole units allow over the resident
+// workgroups; with S = 1 the scales of a workgroup's panels must fit its LDS array.
+static int skinny_grid(int units, int rt, bool split, int resident) {
+  int64_t per = ceil_div(units, resident);
+  if (!split) per = std::min<int64_t>(per, kSkinnyScaleLds / (16 * rt));
+  return (int)ceil_div(units, per);
 }
 
+// The plan of one call for a given configuration: kernel, unit counts, grid and workspace size.
 template <bool I8>
-static SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
+static SkinnyPlan skinny_plan_for(const SkinnyShape& sh, const void* fn, int64_t M, int64_t N,
+                                  int64_t K) {
   SkinnyPlan pl;
-  pl.sh = skinny_shape<I8>(M, N, K);
-  pl.fn = skinny_kernel_for<I8>(pl.sh);
-  pl.x_lds = pl.sh.xlds ? ceil_div(M * (int64_t)skinny_x_row((int)K, I8 ? 1 : 2), 1024) * 1024 : 0;
+  pl.sh = sh;
+  pl.fn = fn;
+  pl.x_lds = sh.xlds ? ceil_div(M * (int64_t)skinny_x_row((int)K, I8 ? 1 : 2), 1024) * 1024 : 0;
   SkinnyArgs& a = pl.a;
   a = SkinnyArgs{};
   a.M = (int)M;
@@ -461,42 +542,73 @@ static SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
   a.K = (int)K;
   a.nsteps = (int)ceil_div(K, kTileK);
   a.nrb = (int)ceil_div(N, kTileRows);
-  a.panels = (int)ceil_div(a.nrb, pl.sh.rt);
-  a.NSU = (int)(ceil_div(ceil_div(a.nsteps, pl.sh.w), pl.sh.dw) * pl.sh.dw);
-  pl.grid = skinny_grid(a.panels, pl.sh.rt, persistent_blocks(pl.fn, 64 * pl.sh.w, pl.x_lds));
+  a.panels = (int)ceil_div(a.nrb, sh.rt);
+  a.splits = sh.splits;
+  a.ssteps = (int)ceil_div(a.nsteps, sh.splits);
+  a.units = a.panels * sh.splits;
+  a.NSU = (int)(ceil_div(ceil_div(a.ssteps, sh.w), sh.dw) * sh.dw);
+  pl.grid = skinny_grid(a.units, sh.rt, sh.splits > 1, persistent_blocks(fn, 64 * sh.w, pl.x_lds));
+  pl.part_bytes = sh.splits > 1 ? (int64_t)sh.splits * M * 16 * a.nrb * 4 : 0;
   return pl;
 }
 
 template <bool I8>
-static int launch_skinny(const void* x, int64_t ldx, const int8_t* qp, const float* s,
-                         const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
-                         int64_t N, int64_t K, hipStream_t stream) {
-  SkinnyPlan pl = skinny_plan<I8>(M, N, K);
+static SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
+  const SkinnyShape sh = skinny_shape<I8>(M, N, K);
+  return skinny_plan_for<I8>(sh, skinny_kernel_for<I8>(sh), M, N, K);
+}
+
+// Launches a planned call: the unit kernel, then (S > 1) the reduction over the splits. The
+// workspace `part` must hold pl.part_bytes.
+template <bool I8>
+static int skinny_launch(SkinnyPlan& pl, void* part, hipStream_t stream) {
+  SkinnyArgs& a = pl.a;
+  a.part = part;
+  void* args[] = {&a};
+  hipError_t e = hipLaunchKernel(pl.fn, dim3((unsigned)pl.grid), dim3(64 * pl.sh.w), args,
+                                 pl.x_lds, stream);
+  if (e == hipSuccess && pl.sh.splits > 1) {
+    const int64_t threads = (int64_t)a.M * 4 * a.nrb;
+    e = hipLaunchKernel(reinterpret_cast<const void*>(&skinny_reduce<I8>),
+                        dim3((unsigned)ceil_div(threads, 256)), dim3(256), args, 0, stream);
+  }
+  return e == hipSuccess ? launch_status() : (int)e;
+}
+
+int64_t skinny_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K) {
+  return i8 ? skinny_plan<true>(M, N, K).part_bytes : skinny_plan<false>(M, N, K).part_bytes;
+}
+
+int launch_w8a16_skinny(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                        uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                        int64_t ws_bytes, hipStream_t stream) {
+  SkinnyPlan pl = skinny_plan<false>(M, N, K);
+  if (ws_bytes < pl.part_bytes || (pl.part_bytes && !ws)) return LSE_E_WORKSPACE;
   SkinnyArgs& a = pl.a;
   a.x = x;
   a.ldx = ldx;
+  a.qp = qp;
+  a.s = s;
+  a.y = y;
+  a.ldy = ldy;
+  return skinny_launch<false>(pl, ws, stream);
+}
+
+int launch_w8a8_skinny(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                       uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
+                       void* ws, int64_t ws_bytes, hipStream_t stream) {
+  SkinnyPlan pl = skinny_plan<true>(M, N, K);
+  if (ws_bytes < pl.part_bytes || (pl.part_bytes && !ws)) return LSE_E_WORKSPACE;
+  SkinnyArgs& a = pl.a;
+  a.x = xq;
+  a.ldx = K;
   a.qp = qp;
   a.s = s;
   a.sx = sx;
   a.y = y;
   a.ldy = ldy;
   a.acc = acc;
-  void* args[] = {&a};
-  const hipError_t e = hipLaunchKernel(pl.fn, dim3((unsigned)pl.grid), dim3(64 * pl.sh.w), args,
-                                       pl.x_lds, stream);
-  return e == hipSuccess ? launch_status() : (int)e;
-}
-
-int launch_w8a16_skinny(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
-                        uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                        hipStream_t stream) {
-  return launch_skinny<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, stream);
-}
-
-int launch_w8a8_skinny(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
-                       uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
-                       hipStream_t stream) {
-  return launch_skinny<true>(xq, K, qp, s, sx, y, ldy, acc, M, N, K, stream);
+  return skinny_launch<true>(pl, ws, stream);
 }
 
 }  // namespace lse

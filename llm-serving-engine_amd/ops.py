@@ -23,6 +23,7 @@ __all__ = [
     "w8a8_gemm",
     "w8a8_linear",
     "w8a16_linear",
+    "workspace",
 ]
 
 
@@ -80,6 +81,19 @@ def unpack_weight(qp: torch.Tensor, n: int, k: int) -> torch.Tensor:
     return t[:n, :k].contiguous()
 
 
+def workspace(mode: int, m: int, n: int, k: int, dev: torch.device) -> torch.Tensor | None:
+    """The workspace one decode-kernel call needs (some shapes add partial sums of K ranges in a
+    second pass), or None. Allocated with torch.empty, so graph-pool owned under capture; the
+    caller keeps it alive until the call is enqueued."""
+    nbytes = _lib.library().lse_workspace_bytes(mode, m, n, k)
+    _require(nbytes >= 0, f"lse_workspace_bytes rejected (M, N, K) = ({m}, {n}, {k})")
+    return torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
+
+
+def _ws_args(ws: torch.Tensor | None) -> tuple[int | None, int]:
+    return (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+
+
 def _check_packed(qp: torch.Tensor, n: int, k: int) -> None:
     _require(qp.dtype == torch.int8 and qp.is_contiguous(), "packed weight must be contiguous int8")
     _require(tuple(qp.shape) == packed_shape(n, k),
@@ -128,10 +142,11 @@ def w8a16_linear(
     m = x2.shape[0]
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     ldx = x2.stride(0) if m > 1 else k
+    ws = workspace(_lib.MODE_W8A16, m, n, k, dev) if algo != _lib.ALGO_PREFILL else None
     _lib.check(
         _lib.library().lse_w8a16_gemm_algo(
             x2.data_ptr(), ldx, qp.data_ptr(), scales.data_ptr(), y.data_ptr(), n,
-            m, n, k, algo, _stream(dev),
+            m, n, k, algo, *_ws_args(ws), _stream(dev),
         ),
         "lse_w8a16_gemm",
     )
@@ -177,11 +192,12 @@ def w8a8_gemm(
     _check_packed(qp, n, k)
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev) if want_y else None
     acc = torch.empty((m, n), dtype=torch.int32, device=dev) if want_acc else None
+    ws = workspace(_lib.MODE_W8A8, m, n, k, dev)
     _lib.check(
         _lib.library().lse_w8a8_gemm(
             xq.data_ptr(), sx.data_ptr(), qp.data_ptr(), scales.data_ptr(),
             y.data_ptr() if y is not None else None, n,
-            acc.data_ptr() if acc is not None else None, m, n, k, _stream(dev),
+            acc.data_ptr() if acc is not None else None, m, n, k, *_ws_args(ws), _stream(dev),
         ),
         "lse_w8a8_gemm",
     )

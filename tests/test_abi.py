@@ -26,7 +26,7 @@ def test_header_declares_the_entry_points():
     names = _declared_functions()
     assert {
         "lse_quantize_weight_per_channel", "lse_packed_weight_bytes", "lse_pack_weight",
-        "lse_w8a16_gemm", "lse_w8a16_gemm_algo",
+        "lse_w8a16_gemm", "lse_w8a16_gemm_algo", "lse_workspace_bytes",
         "lse_quantize_act_per_token", "lse_w8a8_gemm", "lse_query", "lse_status_string",
     } <= names
 
@@ -60,7 +60,7 @@ def test_query_values(pkg):
 
 # A fake, 256-byte-aligned device address: every call below is rejected before it is used.
 FAKE = ctypes.c_void_p(1 << 20)
-E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO = -1, -2, -3, -4, -5
+E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO, E_WORKSPACE = -1, -2, -3, -4, -5, -6
 
 
 @pytest.mark.parametrize(
@@ -90,15 +90,32 @@ E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO = -1, -2, -3, -4, -5
 )
 def test_w8a16_rejects_bad_arguments(pkg, args, status):
     lib = pkg.library()
-    assert lib.lse_w8a16_gemm_algo(*args, None) == status
+    assert lib.lse_w8a16_gemm_algo(*args, None, 0, None) == status
     assert lib.lse_status_string(status)
+
+
+def test_workspace_query_and_rejections(pkg):
+    lib = pkg.library()
+    assert lib.lse_workspace_bytes(0, -1, 64, 64) == -1
+    assert lib.lse_workspace_bytes(2, 1, 64, 64) == -1
+    assert lib.lse_workspace_bytes(0, 65, 4096, 4096) == 0  # prefill kernels need none
+    assert lib.lse_workspace_bytes(1, 0, 4096, 4096) == 0
+    for mode in (0, 1):
+        for m in (1, 16, 17, 33, 64):
+            nbytes = lib.lse_workspace_bytes(mode, m, 4096, 14336)
+            assert 0 <= nbytes <= 64 * m * (4096 + 15) and nbytes % 16 == 0
+    args = (FAKE, 64, FAKE, FAKE, FAKE, 64, 2, 64, 64, 1)
+    assert lib.lse_w8a16_gemm_algo(*args, FAKE, -1, None) == E_WORKSPACE
+    assert lib.lse_w8a16_gemm_algo(*args, ctypes.c_void_p((1 << 20) + 8), 64, None) == E_WORKSPACE
+    assert lib.lse_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, FAKE, -1,
+                             None) == E_WORKSPACE
 
 
 def test_empty_shapes_are_no_ops(pkg):
     lib = pkg.library()
-    assert lib.lse_w8a16_gemm(None, 0, None, None, None, 0, 0, 0, 0, None) == 0
-    assert lib.lse_w8a16_gemm(None, 16, FAKE, FAKE, None, 0, 0, 64, 16, None) == 0
-    assert lib.lse_w8a8_gemm(None, None, FAKE, FAKE, None, 0, None, 0, 64, 16, None) == 0
+    assert lib.lse_w8a16_gemm(None, 0, None, None, None, 0, 0, 0, 0, None, 0, None) == 0
+    assert lib.lse_w8a16_gemm(None, 16, FAKE, FAKE, None, 0, 0, 64, 16, None, 0, None) == 0
+    assert lib.lse_w8a8_gemm(None, None, FAKE, FAKE, None, 0, None, 0, 64, 16, None, 0, None) == 0
     assert lib.lse_quantize_act_per_token(None, 0, None, FAKE, 0, 16, None) == 0
     assert lib.lse_quantize_weight_per_channel(None, 0, None, FAKE, 0, 16, None) == 0
     assert lib.lse_pack_weight(None, 0, 16, None, None) == 0
@@ -124,14 +141,14 @@ def test_quantizers_and_w8a8_reject_bad_arguments(pkg):
     assert lib.lse_quantize_act_per_token(FAKE, 32, FAKE, FAKE, -1, 32, None) == E_SHAPE
     assert lib.lse_quantize_act_per_token(FAKE, 36, FAKE, FAKE, 2, 32, None) == E_ALIGN
     assert lib.lse_quantize_act_per_token(None, 32, FAKE, FAKE, 2, 32, None) == E_NULL
-    assert lib.lse_w8a8_gemm(FAKE, None, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, None) == E_NULL
-    assert lib.lse_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, FAKE, 64, None, 2, 64, 200_000, None) == E_RANGE
+    assert lib.lse_w8a8_gemm(FAKE, None, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, None, 0, None) == E_NULL
+    assert lib.lse_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, FAKE, 64, None, 2, 64, 200_000, None, 0, None) == E_RANGE
     assert lib.lse_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, FAKE, 64, ctypes.c_void_p((1 << 20) + 4),
-                             2, 64, 64, None) == E_ALIGN
-    assert lib.lse_w8a8_gemm(None, FAKE, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, None) == E_NULL
+                             2, 64, 64, None, 0, None) == E_ALIGN
+    assert lib.lse_w8a8_gemm(None, FAKE, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, None, 0, None) == E_NULL
 
 
 def test_status_strings(pkg):
     lib = pkg.library()
-    for st in (0, E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO, -99):
+    for st in (0, E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO, E_WORKSPACE, -99):
         assert isinstance(lib.lse_status_string(st), bytes)

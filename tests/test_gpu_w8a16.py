@@ -30,9 +30,11 @@ def _run(pkg, dev, x_bits, q, s, algo, ldy_pad=0):
     if ldy_pad:
         sentinel = torch.full((m, n + ldy_pad), -7.0, dtype=torch.bfloat16, device=dev)
         lib = pkg.library()
+        ws = pkg.ops.workspace(0, m, n, k, dev) if algo != PREFILL else None
         status = lib.lse_w8a16_gemm_algo(
             x.data_ptr(), k, qt.data_ptr(), st.data_ptr(), sentinel.data_ptr(), n + ldy_pad,
-            m, n, k, algo, torch.cuda.current_stream().cuda_stream,
+            m, n, k, algo, ws.data_ptr() if ws is not None else None,
+            ws.numel() if ws is not None else 0, torch.cuda.current_stream().cuda_stream,
         )
         assert status == 0
         torch.cuda.synchronize()
@@ -75,11 +77,37 @@ def test_decode_all_m_tiles(pkg, dev, m):
 
 
 @pytest.mark.parametrize("m", [1, 16, 17, 32, 33, 64])
-@pytest.mark.parametrize("n,k", [(48, 4096), (4096, 128), (144, 3136), (1000, 1040), (16, 14336)])
+@pytest.mark.parametrize(
+    "n,k", [(48, 4096), (4096, 128), (144, 3136), (1000, 1040), (16, 14336), (1000, 8208)]
+)
 def test_decode_split_panels(pkg, dev, m, n, k):
     """Few panels with a long K, many panels with a short K, a K tail past the last whole unit,
-    and activations both staged whole and streamed through the LDS ring."""
+    and activations both staged whole and streamed through the LDS ring. With more than 16
+    tokens, (16, 14336) and (1000, 8208) split K and add partial sums in a second pass: the
+    latter with a partial last panel, a shorter last K range and a 16-wide K tail."""
     _check(pkg, dev, m, n, k, 11 * m + n + k, DECODE)
+
+
+def test_decode_rejects_a_short_workspace(pkg, dev):
+    """A split-K shape needs a workspace; a smaller one is refused before any launch."""
+    m, n, k = 40, 4096, 14336
+    need = pkg.library().lse_workspace_bytes(0, m, n, k)
+    assert need >= 4 * m * n * 4
+    x = torch.zeros(m, k, dtype=torch.bfloat16, device=dev)
+    qp = torch.zeros(pkg.ops.packed_shape(n, k), dtype=torch.int8, device=dev)
+    s = torch.ones(n, dtype=torch.float32, device=dev)
+    y = torch.full((m, n), 3.0, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = pkg.library()
+    args = (x.data_ptr(), k, qp.data_ptr(), s.data_ptr(), y.data_ptr(), n, m, n, k, DECODE)
+    assert lib.lse_w8a16_gemm_algo(*args, ws.data_ptr(), need - 16, stream) == -6
+    assert lib.lse_w8a16_gemm_algo(*args, None, 0, stream) == -6
+    torch.cuda.synchronize()
+    assert torch.all(y == 3.0)
+    assert lib.lse_w8a16_gemm_algo(*args, ws.data_ptr(), need, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.all(y == 0.0)
 
 
 @pytest.mark.parametrize(

@@ -42,10 +42,11 @@ def test_decode_kernel_bit_exact(pkg, dev, m):
 
 
 @pytest.mark.parametrize("m", [1, 16, 17, 32, 33, 64])
-@pytest.mark.parametrize("n,k", [(48, 4096), (4096, 128), (144, 3136), (16, 14336)])
+@pytest.mark.parametrize("n,k", [(48, 4096), (4096, 128), (144, 3136), (16, 14336), (1000, 8208)])
 def test_decode_split_panels_bit_exact(pkg, dev, m, n, k):
     """Few panels with a long K and many panels with a short K, staged and streamed
-    activations: the int32 sums stay exact."""
+    activations, and (past 16 tokens) K split over four partial sums added in a second pass:
+    the int32 sums stay exact."""
     _check(pkg, dev, m, n, k, 7 * m + n + k)
 
 
