@@ -12,6 +12,19 @@ M sweep) and config 3 (W8A8 quantize + int8 GEMM, TOP/s), plus the roofline of t
 kernel and the CPU baseline (the reference's bf16 F.linear on the host cores).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-secondary]
+
+Profiling (the decode sweep alone, then a CPU-side summary of the rocprofv3 output):
+
+    rocprofv3 --kernel-trace --stats -d T -o run --output-format csv -- \
+        python3 bench.py --only decode --steps 5 --warmup 2
+    rocprofv3 --pmc FETCH_SIZE -d F -o run --output-format csv -- \
+        python3 bench.py --only decode --steps 1 --warmup 0
+    rocprofv3 --pmc WRITE_SIZE -d W -o run --output-format csv -- \
+        python3 bench.py --only decode --steps 1 --warmup 0
+    python3 bench.py --summarize-profiles T F W
+
+`--only decode` first runs one plain 64 MiB elementwise copy (int32 bitwise_not: 64 MiB read,
+64 MiB written), whose FETCH_SIZE and WRITE_SIZE readings scale the counters to bytes.
 """
 
 from __future__ import annotations
@@ -33,6 +46,9 @@ DECODE_MS = [1, 8, 32, 64]
 PREFILL_MS = [512, 2048, 8192]
 W8A8_MS = [1, 32, 512, 4096]
 LAYERS = 8
+CALIBRATION_BYTES = 64 << 20
+PROFILE_MD = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.md"
+PROFILE_TRAFFIC = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.traffic.json"
 
 
 def decode_bytes(m: int, k: int, n: int) -> int:
@@ -47,6 +63,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true", help="skip prefill and W8A8 figures")
     p.add_argument("--only", choices=["decode", "prefill", "w8a8"], help="profile one family")
+    p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
+                   help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
     return p.parse_args()
 
 
@@ -79,6 +97,19 @@ def time_region(fn, steps: int, warmup: int) -> float:
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / 1e3
+
+
+def calibration_copy(dev) -> None:
+    """One plain elementwise copy of CALIBRATION_BYTES (int32 bitwise_not), the reference reading
+    for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def bench_decode(pkg, dev, steps: int, warmup: int, gen) -> dict:
@@ -194,8 +225,148 @@ def bench_w8a8(pkg, dev, steps: int, gen) -> dict:
     return res
 
 
+# ---- profile summaries (CPU only: reads rocprofv3 CSV output) ---------------------------------
+
+SWEEP_CALLS = [(m, si) for m in DECODE_MS for _ in range(LAYERS) for si in range(len(SHAPES))]
+
+
+def _decode_calls(records: list[dict]) -> list[list[dict]]:
+    """Dispatch records (in dispatch order) grouped into decode GEMM calls: a skinny_kernel
+    dispatch, plus the skinny_reduce dispatch that follows it when K is split."""
+    calls: list[list[dict]] = []
+    for r in records:
+        name = r["Kernel_Name"]
+        if "skinny_kernel" in name:
+            calls.append([r])
+        elif "skinny_reduce" in name:
+            calls[-1].append(r)
+    return calls
+
+
+def _short(name: str) -> str:
+    return name.split("(")[0].replace("void ", "")
+
+
+def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> None:
+    import csv
+    import statistics
+
+    def read(path):
+        with open(path, newline="") as f:
+            return list(csv.DictReader(f))
+
+    n = len(SWEEP_CALLS)
+    trace = read(Path(trace_dir) / "run_kernel_trace.csv")
+    trace.sort(key=lambda r: int(r["Start_Timestamp"]))
+    calls = _decode_calls(trace)
+    passes = len(calls) // n
+    # Pass 0 is the eager run before capture; the sweep graph's replays follow (warmup + steps),
+    # then the per-M and per-shape graphs, which are not used here.
+    replays = [calls[i * n:(i + 1) * n] for i in range(1, passes)]
+    replays = [r for r in replays
+               if [_short(c[0]["Kernel_Name"]) for c in r] ==
+               [_short(c[0]["Kernel_Name"]) for c in calls[:n]]][:7]
+    span = {}
+    for i in range(n):
+        span[i] = statistics.median(
+            (int(r[i][-1]["End_Timestamp"]) - int(r[i][0]["Start_Timestamp"])) / 1e3
+            for r in replays)
+
+    def counters(d, counter):
+        rows = [r for r in read(Path(d) / "run_counter_collection.csv")
+                if r["Counter_Name"] == counter]
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        calib = [float(r["Counter_Value"]) for r in rows if "bitwise_not" in r["Kernel_Name"]]
+        factor = CALIBRATION_BYTES / (calib[0] * 1024)
+        per_call = [sum(float(r["Counter_Value"]) for r in c) * 1024 * factor
+                    for c in _decode_calls(rows)[:n]]
+        return factor, calib[0], per_call
+
+    ff, fkib, fetch = counters(fetch_dir, "FETCH_SIZE")
+    wf, wkib, write = counters(write_dir, "WRITE_SIZE")
+
+    stats = read(Path(trace_dir) / "run_kernel_stats.csv")
+    cmds = [
+        "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_decode -o run --output-format csv "
+        "-- python3 bench.py --only decode --steps 5 --warmup 2",
+        "rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o run --output-format csv "
+        "-- python3 bench.py --only decode --steps 1 --warmup 0",
+        "rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o run --output-format csv "
+        "-- python3 bench.py --only decode --steps 1 --warmup 0",
+        "python3 bench.py --summarize-profiles gpurun_out/prof_decode gpurun_out/pmc_fetch "
+        "gpurun_out/pmc_write",
+    ]
+    out = ["# skinny_kernel (+ skinny_reduce) — config-1 W8A16 decode sweep", "",
+           "Llama-3-8B shapes (K, N) in {(4096,6144), (4096,4096), (4096,28672), (14336,4096)} x "
+           f"M in {DECODE_MS}, {LAYERS} weight copies rotated, one MI355X.", "",
+           "Commands (repository root, one MI355X; the last runs on any host):", "", "```",
+           *cmds, "```", "",
+           "## rocprofv3 --stats (whole profiled run)", "",
+           "| kernel | calls | avg us | total ms |", "|---|---|---|---|"]
+    for r in stats:
+        if "skinny" in r["Name"] or "bitwise_not" in r["Name"]:
+            out.append(f"| `{_short(r['Name'])[:90]}` | {r['Calls']} | "
+                       f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['TotalDurationNs']) / 1e6:.2f} |")
+    out += ["", f"## Per call (median over {len(replays)} replays of the sweep graph; a call is the "
+            "skinny_kernel dispatch plus, when K is split, its skinny_reduce)", "",
+            "HBM bytes = FETCH_SIZE x 1024 x "
+            f"{ff:.3f} + WRITE_SIZE x 1024 x {wf:.3f}: the 64 MiB calibration copy read "
+            f"{fkib:.1f} KiB of FETCH_SIZE and {wkib:.1f} KiB of WRITE_SIZE.", "",
+            "| M | shape (K,N) | kernel | us | algorithmic MB | HBM MB (PMC) | GB/s | frac of 8 TB/s |",
+            "|---|---|---|---|---|---|---|---|"]
+    tot_t = tot_b = tot_h = 0.0
+    seen = set()
+    for i, (m, si) in enumerate(SWEEP_CALLS):
+        k, nn = SHAPES[si]
+        b = decode_bytes(m, k, nn)
+        tot_t += span[i]
+        tot_b += b
+        tot_h += fetch[i] + write[i]
+        if (m, si) in seen:
+            continue
+        seen.add((m, si))
+        same = [j for j, c in enumerate(SWEEP_CALLS) if c == (m, si)]
+        t = statistics.median(span[j] for j in same)
+        h = statistics.median(fetch[j] + write[j] for j in same)
+        names = " + ".join(sorted({_short(r["Kernel_Name"]).replace("lse::", "")
+                                   for j in same for r in replays[0][j]}))
+        out.append(f"| {m} | {SHAPE_NAMES[si]} ({k},{nn}) | `{names}` | {t:.2f} | {b / 1e6:.2f} | "
+                   f"{h / 1e6:.2f} | {b / t / 1e3:.0f} | {b / t / 1e3 / HBM_PEAK_GBPS:.3f} |")
+    avg_b, avg_h, avg_t = tot_b / n, tot_h / n, tot_t / n
+    out += ["", f"Sweep of {n} calls: sum of per-call medians {tot_t:.1f} us; "
+            f"{tot_b / 1e9:.3f} GB algorithmic -> {tot_b / tot_t / 1e3:.0f} GB/s "
+            f"({tot_b / tot_t / 1e3 / HBM_PEAK_GBPS:.3f} of 8 TB/s). Average per call: "
+            f"{avg_b / 1e6:.2f} MB algorithmic, {avg_h / 1e6:.2f} MB HBM traffic "
+            f"({avg_h / avg_b:.3f}x), {avg_t:.2f} us."]
+    PROFILE_MD.write_text("\n".join(out) + "\n")
+    PROFILE_TRAFFIC.write_text(json.dumps({
+        "workload": "config1 W8A16 decode sweep",
+        "calls": n,
+        "algorithmic_bytes_per_call": round(avg_b),
+        "hbm_bytes_per_call": round(avg_h),
+        "fetch_factor": round(ff, 4),
+        "write_factor": round(wf, 4),
+        "median_us_per_call": round(avg_t, 3),
+    }, indent=1) + "\n")
+    print("\n".join(out))
+
+
+def measured_traffic(dec: dict) -> float | None:
+    """HBM bytes per decode call from the committed PMC summary of this same sweep, or None."""
+    try:
+        t = json.loads(PROFILE_TRAFFIC.read_text())
+    except (OSError, ValueError):
+        return None
+    if t.get("calls") != dec["launches_per_step"]:
+        return None
+    return t["hbm_bytes_per_call"]
+
+
 def main() -> None:
     args = parse()
+    if args.summarize_profiles:
+        summarize_profiles(*args.summarize_profiles)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the int8 Linear "
               "path runs on a single MI355X; multi-GPU sharding is a design note only)",
@@ -210,6 +381,8 @@ def main() -> None:
     gen = torch.Generator().manual_seed(1000)
     out: dict = {}
 
+    if args.only == "decode":
+        calibration_copy(dev)
     if args.only in (None, "decode"):
         dec = bench_decode(pkg, dev, args.steps, args.warmup, gen)
     if args.only == "prefill":
@@ -266,7 +439,7 @@ def main() -> None:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dec),
         },
         "cpu_baseline": cpu,
         "decode_by_m_gbps": dec["by_m_gbps"],
