@@ -61,7 +61,6 @@ int persistent_blocks(const void* kernel, int threads, size_t dyn_lds) {
 namespace {
 
 constexpr int64_t kMaxGridX = 2147483647;
-constexpr int64_t kMaxGridY = 65535;
 constexpr int64_t kMaxRows = 2147483647;  // row indices are int inside the kernels
 constexpr uint32_t kBufferLimit = lse::kOutOfRange;  // byte extent of a buffer resource
 
@@ -182,7 +181,8 @@ int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const floa
     return lse::launch_w8a16_skinny((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K,
                                     workspace, workspace_bytes, st);
   }
-  if ((M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
+  // The tiled kernel addresses a block's 256 rows of x through a 32-bit buffer resource.
+  if (256 * ldx * 2 >= (int64_t)kBufferLimit) return LSE_E_RANGE;
   return lse::launch_w8a16_gemm((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K, st);
 }
 
@@ -221,7 +221,7 @@ int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const flo
     return lse::launch_w8a8_skinny(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, workspace,
                                    workspace_bytes, st);
   }
-  if ((M + 127) / 128 > kMaxGridY) return LSE_E_RANGE;
+  if (256 * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
   return lse::launch_w8a8_gemm(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, st);
 }
 

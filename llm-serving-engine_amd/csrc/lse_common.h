@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #include "lse_int8.h"
 
 namespace lse {
@@ -86,6 +88,93 @@ constexpr int kTileK = 64;
 constexpr int kTileBytes = 1024;
 
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// The scaled output of one lane's MFMA result: `v` holds rows n..n+3 (cnt of them valid) of
+// token m, `sc` their scales, sxm the token's scale (W8A8). W8A16: y = bf16(v * s[n]); W8A8:
+// acc = v (int32, when acc is not null; row stride N), y = bf16((v * sx[m]) * s[n]) (when y is
+// not null). yvec: y rows allow an aligned 8-byte store of four outputs.
+template <bool I8, typename Acc>
+__device__ __forceinline__ void store_out4(uint16_t* y, int64_t ldy, int32_t* acc, int N, int m,
+                                           int n, int cnt, Acc v, const float (&sc)[4], float sxm,
+                                           bool yvec) {
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if constexpr (I8)
+      o[r] = ((float)v[r] * sxm) * sc[r];
+    else
+      o[r] = v[r] * sc[r];
+  }
+  if constexpr (I8) {
+    if (acc) {
+      int32_t* dst = acc + (int64_t)m * N + n;
+      if (cnt == 4 && (N & 3) == 0) {
+        *reinterpret_cast<i32x4*>(dst) = v;
+      } else {
+        for (int r = 0; r < cnt; ++r) dst[r] = v[r];
+      }
+    }
+    if (!y) return;
+  }
+  uint16_t* out = y + (int64_t)m * ldy + n;
+  if (cnt == 4 && yvec) {
+    *reinterpret_cast<uint2*>(out) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+  } else {
+    for (int r = 0; r < cnt; ++r) out[r] = f32_to_bf16(o[r]);
+  }
+}
+
+// s_waitcnt immediate that waits for all but the `n` most recent vector-memory operations
+// (vmcnt = n, expcnt and lgkmcnt left at their maxima).
+__host__ __device__ constexpr int vmcnt_imm(int n) {
+  return (n & 15) | 0x70 | 0xF00 | ((n >> 4) << 14);
+}
+
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+// Direct-to-LDS 16-byte buffer load: lane l's 16 bytes from `offset` land at lds + 16 l (lds is
+// wave-uniform). An offset past the resource writes zeros and issues no memory request.
+__device__ __forceinline__ void buffer_load16_lds(BufferRsrc r, void* lds, uint32_t offset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, offset, 0, 0, 0);
+}
+
+// The same load with the buffer descriptor as four dwords, issued from inline assembly. The
+// compiler then does not track the LDS write, so it inserts no waits of its own between these
+// loads and later LDS reads: the caller orders them with explicit s_waitcnt vmcnt counts and
+// barriers (vmcnt drops when the data is in LDS). M0 carries the LDS address and is restored.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 make_rsrc4(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// LDS byte address of a shared-memory pointer, as a wave-uniform value.
+__device__ __forceinline__ uint32_t lds_addr(const void* lds) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)lds);
+}
+
+// One load to LDS byte address base + IMM (+ 16 l for lane l).
+template <int IMM>
+__device__ __forceinline__ void dma16_lds(u32x4 r, uint32_t base, uint32_t offset) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_add_u32 m0, %1, %4\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(base), "v"(offset), "s"(r), "i"(IMM)
+      : "memory", "scc");
+}
+
+// N loads, load i to base + i * STEP, from offsets off[i].
+template <int STEP, int... I>
+__device__ __forceinline__ void dma16_lds_seq(u32x4 r, uint32_t base, const uint32_t* off,
+                                              std::integer_sequence<int, I...>) {
+  (dma16_lds<I * STEP>(r, base, off[I]), ...);
+}
 
 // Workgroups of `kernel` (launched with `threads` threads and `dyn_lds` bytes of dynamic LDS)
 // that fit on the current device at once: CU count x resident workgroups per CU. Persistent

@@ -66,50 +66,11 @@ struct SkinnyArgs {
   void* part;           // S > 1: raw partial sums [S][M][16 nrb], fp32 (W8A16) or int32 (W8A8)
 };
 
-// The scaled output of one lane: `v` holds rows n..n+3 (cnt of them valid) of token m, `sc` their
-// scales, sxm the token's scale (W8A8). W8A16: y = bf16(v * s[n]); W8A8: acc = v (int32, when
-// requested), y = bf16((v * sx[m]) * s[n]).
-template <bool I8, typename Acc>
-__device__ __forceinline__ void skinny_epilogue(const SkinnyArgs& a, int m, int n, int cnt, Acc v,
-                                                const float (&sc)[4], float sxm, bool yvec) {
-  float o[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if constexpr (I8)
-      o[r] = ((float)v[r] * sxm) * sc[r];
-    else
-      o[r] = v[r] * sc[r];
-  }
-  if constexpr (I8) {
-    if (a.acc) {
-      int32_t* dst = a.acc + (int64_t)m * a.N + n;
-      if (cnt == 4 && (a.N & 3) == 0) {
-        *reinterpret_cast<i32x4*>(dst) = v;
-      } else {
-        for (int r = 0; r < cnt; ++r) dst[r] = v[r];
-      }
-    }
-    if (!a.y) return;
-  }
-  uint16_t* out = a.y + (int64_t)m * a.ldy + n;
-  if (cnt == 4 && yvec) {
-    *reinterpret_cast<uint2*>(out) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
-  } else {
-    for (int r = 0; r < cnt; ++r) out[r] = f32_to_bf16(o[r]);
-  }
-}
-
 // Register stage of the weight ring: one 1 KB tile per row tile of the panel.
 template <int RT>
 struct SkinnyWStage {
   uint4 w[RT];
 };
-
-// s_waitcnt immediate that waits for all but the `n` most recent vector-memory operations
-// (vmcnt = n, expcnt and lgkmcnt left at their maxima).
-__host__ __device__ constexpr int vmcnt_imm(int n) {
-  return (n & 15) | 0x70 | 0xF00 | ((n >> 4) << 14);
-}
 
 // Bytes of one whole-staged activation row: K rounded up to whole 64-wide steps.
 __host__ __device__ constexpr int skinny_x_row(int K, int esz) { return ((K + 63) / 64) * 64 * esz; }
@@ -358,7 +319,7 @@ skinny_kernel(SkinnyArgs a) {
     float sc[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) sc[r] = r < cnt ? s_lds[n + r - srow0] : 0.0f;
-    skinny_epilogue<I8>(a, m, n, cnt, v, sc, sxv[b], yvec);
+    store_out4<I8>(a.y, a.ldy, a.acc, a.N, m, n, cnt, v, sc, sxv[b], yvec);
   };
 
   // End of a unit (panel p of split sp): pass i adds slices [i W, i W + RSLOTS) over the waves in
@@ -446,7 +407,7 @@ skinny_reduce(SkinnyArgs a) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) sc[r] = r < cnt ? a.s[n + r] : 0.0f;
   const bool yvec = a.y && (a.ldy & 3) == 0 && ((uintptr_t)a.y & 7) == 0;
-  skinny_epilogue<I8>(a, m, n, cnt, v, sc, I8 ? a.sx[m] : 0.0f, yvec);
+  store_out4<I8>(a.y, a.ldy, a.acc, a.N, m, n, cnt, v, sc, I8 ? a.sx[m] : 0.0f, yvec);
 }
 
 // ---- host side -----------------------------------------------------------------------------

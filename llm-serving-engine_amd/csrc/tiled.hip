@@ -1,0 +1,338 @@
+// Tiled int8-weight GEMM for M above the decode range, both modes of the int8 Linear:
+//   W8A16: y[m,n] = bf16(s[n] * sum_k x[m,k] q[n,k])               bf16 x, fp32 accumulation
+//   W8A8:  acc[m,n] = sum_k xq[m,k] q[n,k] exactly in int32;  y = bf16((acc * sx[m]) * s[n])
+//
+// MFMA-bound. A block of WGM x WGN = 2 x 4 waves (two per SIMD, so one wave's LDS reads and
+// dequantization overlap the other's MFMAs) computes a BM (tokens) x BN (weight rows) tile of y
+// over K in 64-wide steps; wave (wm, wn) owns a WM x WN sub-tile (128 x 64 for the big tile) of
+// 16x16 MFMA tiles whose A operand is a packed 1 KB weight tile (16 rows x 64 K-bytes, already
+// in operand order) and whose B operand is 16 tokens of x. Per stage a wave dequantizes its
+// weight tiles once, then walks its token tiles, reading each x fragment from LDS once.
+//
+// Data movement (per 64-wide K step, "stage"):
+//  * x rows and the block's packed weight tiles travel HBM/L2 -> LDS by direct-to-LDS buffer
+//    loads (16 bytes per lane, 1 KB per wave instruction) into a ring of NST stage slots, NST-1
+//    stages ahead of the MFMAs. Waits are static vmcnt counts: every stage issues the same loads
+//    (out-of-range ones read zeros and move no data). The loads are issued by dma16_lds, which
+//    the compiler does not track, so the only waits on them are the ones written here.
+//  * Weights stay int8 in LDS (half the footprint and fill traffic of bf16); in W8A16 each wave
+//    dequantizes its WN/16 tiles after the LDS read (exact: |q| <= 127), 1.5 VALU ops per
+//    weight, shared by the WM/16 token tiles it multiplies.
+//  * x rows are stored 16-byte-chunk swizzled (chunk c of row r at c ^ swz(r)) so the 16 rows a
+//    fragment read touches at one K offset fall into distinct banks.
+//  * One barrier per stage: after it, the stage's loads from every wave have landed and every
+//    wave has finished reading the slot the next loads overwrite.
+//
+// Tile order. Blocks are dispatched round-robin over the 8 XCDs; the tile index is remapped so
+// each XCD runs a contiguous range of tiles, in groups of kGroupM token blocks x consecutive
+// weight panels (token blocks fastest within a group). The ~32 blocks resident at once on one
+// XCD then form a 4 x 8 rectangle of tiles whose x and weight panels they share through that
+// XCD's L2: per tile step, a quarter of the operand bytes come from beyond L2 compared with a
+// 32 x 1 strip.
+//
+// Summation order: the K steps in increasing order, two K=32 MFMAs per step (W8A16) in a fixed
+// chain per output; it depends only on K. int32 accumulation (W8A8) is exact in any order.
+#include <algorithm>
+#include <type_traits>
+
+#include "lse_common.h"
+
+namespace lse {
+
+struct TiledArgs {
+  const void* x;     // W8A16: bf16 (M rows, stride ldx); W8A8: int8 xq (M rows, stride ldx)
+  int64_t ldx;       // elements
+  const int8_t* qp;  // packed weight tiles
+  const float* s;    // (N) per-channel scales
+  const float* sx;   // (M) per-token scales, W8A8 only
+  uint16_t* y;       // (M, N) bf16, stride ldy; may be null in W8A8
+  int64_t ldy;
+  int32_t* acc;      // (M, N) int32 contiguous, W8A8 only; may be null
+  int M, N, K;
+  int nsteps;        // ceil(K / 64)
+  int nrb;           // ceil(N / 16)
+  int mblocks, nblocks;
+};
+
+constexpr int kGroupM = 4;
+constexpr int kTiledWgm = 2, kTiledWgn = 4;
+constexpr int kTiledThreads = 64 * kTiledWgm * kTiledWgn;
+
+template <bool I8>
+__device__ __forceinline__ int tiled_swz(int r) {
+  // bf16 rows are 128 bytes (8 chunks, half the banks): rows 2i and 2i+1 cover both halves, so
+  // (r >> 1) spreads 16 rows over all 64 banks. int8 rows are 64 bytes (4 chunks, a quarter).
+  return I8 ? (r >> 2) & 3 : (r >> 1) & 7;
+}
+
+template <bool I8, int BM, int BN, int WGM, int WGN, int NST>
+__global__ void __launch_bounds__(64 * WGM * WGN)
+tiled_gemm_kernel(TiledArgs a) {
+  using Acc = std::conditional_t<I8, i32x4, f32x4>;
+  constexpr int W = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int ESZ = I8 ? 1 : 2;
+  constexpr int XROW = 64 * ESZ;            // bytes of one x row per stage
+  constexpr int XCH = XROW / 16;            // 16-byte chunks per row
+  constexpr int XBYTES = BM * XROW;         // x bytes per stage
+  constexpr int WTILES = BN / 16;           // weight tiles per stage
+  constexpr int XI = XBYTES / (W * 1024);   // direct-to-LDS loads per wave per stage, x
+  constexpr int WI = WTILES / W;            // ... weights
+  constexpr int LOADS = XI + WI;
+  static_assert(TM >= 1 && TN >= 1, "wave grid must tile the block");
+  static_assert(XBYTES % (W * 1024) == 0 && WTILES % W == 0, "whole 1 KB loads per wave");
+  static_assert(NST >= 3 && NST <= 4, "three or four stage slots");
+  static_assert((NST - 2) * LOADS < 64, "vmcnt holds at most 63");
+
+  // One LDS array per stage slot (x image, then the weight tiles).
+  constexpr int SLOT = (XBYTES + WTILES * 1024) / 16;
+  __shared__ uint4 st0[SLOT], st1[SLOT], st2[SLOT], st3[NST > 3 ? SLOT : 1];
+  auto xslot = [&](int i) -> uint4* {
+    switch (i) {
+      case 0: return st0;
+      case 1: return st1;
+      case 2: return st2;
+      default: return st3;
+    }
+  };
+  auto wslot = [&](int i) -> uint4* { return xslot(i) + XBYTES / 16; };
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int r16 = lane & 15, g = lane >> 4;
+
+  // XCD-aware tile order (see the header comment): XCD x = b % 8 receives blocks x, x + 8, ...;
+  // give it the contiguous tile range starting at the tiles of XCDs before it.
+  const int T = a.mblocks * a.nblocks;
+  const int b = blockIdx.x, xcd = b & 7, l = b >> 3, q8 = T >> 3, rem = T & 7;
+  const int t = xcd * q8 + min(xcd, rem) + l;
+  const int group = t / (kGroupM * a.nblocks), first_bm = group * kGroupM;
+  const int gm = min(a.mblocks - first_bm, kGroupM);
+  const int tg = t - group * kGroupM * a.nblocks;
+  const int bm = first_bm + tg % gm, bn = tg / gm;
+  const int m0 = bm * BM, n0 = bn * BN, rb0 = n0 / 16;
+
+  // Buffer resources based at the block's first row / row tile, so 32-bit offsets suffice.
+  const int rows = min(BM, a.M - m0);
+  const u32x4 xres = make_rsrc4(static_cast<const char*>(a.x) + (int64_t)m0 * a.ldx * ESZ,
+                                (uint32_t)(((int64_t)(rows - 1) * a.ldx + a.K) * ESZ));
+  const int rtiles = min(WTILES, a.nrb - rb0);
+  const u32x4 qres = make_rsrc4(a.qp + (int64_t)rb0 * a.nsteps * kTileBytes,
+                                (uint32_t)rtiles * (uint32_t)a.nsteps * kTileBytes);
+
+  // Lane l of load i of a stage fills byte 1024 (wave + W i) + 16 l of the slot's x image: row
+  // r = RPL (wave + W i) + l / XCH (RPL = 1024 / XROW rows per load), physical chunk l % XCH,
+  // which holds logical chunk (l % XCH) ^ swz(r). W RPL is a multiple of 8, so swz(r) is the same
+  // for every i and the lane's K byte is fixed; only the row moves, by W RPL per load.
+  constexpr int RPL = 1024 / XROW;
+  static_assert((W * RPL) % 8 == 0, "swizzle must not depend on the load index");
+  const int x_r0 = RPL * wave + lane / XCH;
+  const int x_kb = 16 * ((lane % XCH) ^ tiled_swz<I8>(x_r0));
+  const int64_t x_step = (int64_t)W * RPL * a.ldx * ESZ;
+  const uint32_t x_base = (uint32_t)((int64_t)x_r0 * a.ldx * ESZ + x_kb);
+  // LDS byte addresses of this wave's first x piece and first weight tile in each slot; load i
+  // goes W KB further.
+  uint32_t x_lds[NST], w_lds[NST];
+#pragma unroll
+  for (int i = 0; i < NST; ++i) {
+    x_lds[i] = lds_addr(xslot(i) + 64 * wave);
+    w_lds[i] = lds_addr(wslot(i) + 64 * wave);
+  }
+  auto load_stage = [&](int kt, int slot) {
+    const bool kv = kt < a.nsteps && XROW * kt + x_kb < a.K * ESZ;
+    uint32_t xo[XI], wo[WI];
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+      const bool rv = x_r0 + W * RPL * i < rows;
+      xo[i] = kv && rv ? x_base + (uint32_t)(i * x_step) + XROW * kt : kOutOfRange;
+    }
+    const bool live = kt < a.nsteps;
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
+      const int tile = wave + W * i;
+      wo[i] = live && tile < rtiles
+                  ? ((uint32_t)tile * (uint32_t)a.nsteps + (uint32_t)kt) * kTileBytes + 16u * lane
+                  : kOutOfRange;
+    }
+    dma16_lds_seq<1024 * W>(xres, x_lds[slot], xo, std::make_integer_sequence<int, XI>{});
+    dma16_lds_seq<1024 * W>(qres, w_lds[slot], wo, std::make_integer_sequence<int, WI>{});
+  };
+
+  Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+
+  auto compute = [&](int slot) {
+    const uint4* xs = xslot(slot);
+    const uint4* ws = wslot(slot) + 64 * wn * TN + lane;
+    if constexpr (I8) {
+      uint4 wv[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) wv[j] = ws[64 * j];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WM + 16 * i + r16;
+        const uint4 xv = xs[r * XCH + (g ^ tiled_swz<I8>(r))];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_i8(wv[j], xv, acc[i][j]);
+      }
+    } else {
+      bf16x8 lo[TN], hi[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) dequant16(ws[64 * j], lo[j], hi[j]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WM + 16 * i + r16;
+        const int sw = tiled_swz<I8>(r);
+        const uint4 x0 = xs[r * XCH + ((2 * g) ^ sw)];
+        const uint4 x1 = xs[r * XCH + ((2 * g + 1) ^ sw)];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          acc[i][j] = mfma16x16x32(lo[j], as_bf16x8(x0), acc[i][j]);
+          acc[i][j] = mfma16x16x32(hi[j], as_bf16x8(x1), acc[i][j]);
+        }
+      }
+    }
+  };
+
+  // Prologue: stages 0 .. NST-2 in flight.
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i) load_stage(i, i);
+  for (int kt0 = 0; kt0 < a.nsteps; kt0 += NST) {
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+      const int kt = kt0 + i;
+      // This wave's loads of stage kt landed (the NST-2 later stages may still be in flight);
+      // after the barrier every wave's have, and slot (i - 1) is no longer read.
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+      __builtin_amdgcn_s_barrier();
+      load_stage(kt + NST - 1, (i + NST - 1) % NST);
+      if (kt < a.nsteps) compute(i);
+    }
+  }
+
+  // The last stages' loads (past K, so they moved no data) are drained before the epilogue.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // Epilogue. D tile (i, j): lane holds weight rows 4 g + r (r = 0..3) of token r16.
+  const bool yvec = a.y && (a.ldy & 3) == 0 && ((uintptr_t)a.y & 7) == 0;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WM + 16 * i + r16;
+    if (m >= a.M) continue;
+    const float sxm = I8 ? a.sx[m] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * WN + 16 * j + 4 * g;
+      if (n >= a.N) continue;
+      const int cnt = min(4, a.N - n);
+      float sc[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = r < cnt ? a.s[n + r] : 0.0f;
+      store_out4<I8>(a.y, a.ldy, a.acc, a.N, m, n, cnt, acc[i][j], sc, sxm, yvec);
+    }
+  }
+}
+
+// ---- host side -----------------------------------------------------------------------------
+
+struct TiledShape {
+  int bm, bn;
+};
+
+template <bool I8, int BM, int BN>
+static const void* tiled_fn() {
+  // LDS per block: NST x (x stage + weight stage) <= 160 KB; 128 x 128 tiles keep two blocks
+  // per CU.
+  constexpr int nst = I8 ? 4 : 3;
+  return reinterpret_cast<const void*>(
+      &tiled_gemm_kernel<I8, BM, BN, kTiledWgm, kTiledWgn, nst>);
+}
+
+template <bool I8>
+static const void* tiled_kernel_for(const TiledShape& sh) {
+  if (sh.bm == 256 && sh.bn == 256) return tiled_fn<I8, 256, 256>();
+  if (sh.bm == 256 && sh.bn == 128) return tiled_fn<I8, 256, 128>();
+  if (sh.bm == 128 && sh.bn == 256) return tiled_fn<I8, 128, 256>();
+  return tiled_fn<I8, 128, 128>();
+}
+
+// The tile that minimizes (rounds of resident blocks) x (CU time per round) = rounds x tile area
+// x blocks per CU / relative efficiency: big tiles need fewer LDS bytes per MFMA, small tiles fill
+// the CUs when there are few tiles. Efficiencies relative to 256 x 256, measured on MI355X at
+// M = 8192 (many rounds).
+static TiledShape tiled_shape(int64_t M, int64_t N, int cus) {
+  static const TiledShape cand[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+  static const double eff[] = {1.0, 0.79, 0.85, 0.85};
+  static const int per_cu[] = {1, 1, 1, 2};
+  TiledShape best = cand[0];
+  double best_cost = 1e300;
+  for (int i = 0; i < 4; ++i) {
+    const int64_t blocks = ceil_div(M, cand[i].bm) * ceil_div(N, cand[i].bn);
+    const int64_t rounds = ceil_div(blocks, (int64_t)cus * per_cu[i]);
+    const int64_t sharing = std::min<int64_t>(per_cu[i], ceil_div(blocks, cus));  // blocks per CU
+    const double cost = (double)rounds * cand[i].bm * cand[i].bn * sharing / eff[i];
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = cand[i];
+    }
+  }
+  return best;
+}
+
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  return cus;
+}
+
+template <bool I8>
+static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const float* s,
+                        const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
+                        int64_t N, int64_t K, hipStream_t stream) {
+  const TiledShape sh = tiled_shape(M, N, device_cus());
+  TiledArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.qp = qp;
+  a.s = s;
+  a.sx = sx;
+  a.y = y;
+  a.ldy = ldy;
+  a.acc = acc;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.nsteps = (int)ceil_div(K, kTileK);
+  a.nrb = (int)ceil_div(N, kTileRows);
+  a.mblocks = (int)ceil_div(M, sh.bm);
+  a.nblocks = (int)ceil_div(N, sh.bn);
+  const int64_t blocks = (int64_t)a.mblocks * a.nblocks;
+  if (blocks > 0x7fffffff) return LSE_E_RANGE;
+  void* args[] = {&a};
+  const hipError_t e = hipLaunchKernel(tiled_kernel_for<I8>(sh), dim3((unsigned)blocks),
+                                       dim3(kTiledThreads), args, 0, stream);
+  return e == hipSuccess ? launch_status() : (int)e;
+}
+
+int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                      uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                      hipStream_t stream) {
+  return launch_tiled<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, stream);
+}
+
+int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                     uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
+                     hipStream_t stream) {
+  return launch_tiled<true>(xq, K, qp, s, sx, y, ldy, acc, M, N, K, stream);
+}
+
+}  // namespace lse

@@ -86,6 +86,7 @@ E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO, E_WORKSPACE = -1, -2, -3, -4, -5, -6
         ((FAKE, 64, FAKE, FAKE, FAKE, 64, 1, 64, 64, 7), E_ALGO),
         ((FAKE, 1 << 20, FAKE, FAKE, FAKE, 64, 1, 64, 200_000, 0), E_RANGE),
         ((FAKE, 4096, FAKE, FAKE, FAKE, 1 << 20, 1, 1 << 20, 4096, 0), E_RANGE),
+        ((FAKE, 1 << 23, FAKE, FAKE, FAKE, 64, 100, 64, 64, 2), E_RANGE),  # tiled x extent
     ],
 )
 def test_w8a16_rejects_bad_arguments(pkg, args, status):
