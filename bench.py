@@ -62,7 +62,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true", help="skip prefill and W8A8 figures")
-    p.add_argument("--only", choices=["decode", "prefill", "w8a8"], help="profile one family")
+    p.add_argument("--only", choices=["decode", "prefill", "w8a8", "decode-step"],
+                   help="one family; decode-step is config 4 (a 32-layer model's decode step)")
     p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
                    help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
     return p.parse_args()
@@ -362,6 +363,96 @@ def measured_traffic(dec: dict) -> float | None:
     return t["hbm_bytes_per_call"]
 
 
+def time_graph(fn, steps: int) -> float:
+    """Seconds per replay of fn captured into one graph."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return time_region(g.replay, steps, 1) / steps
+
+
+def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
+                      context: int = 1024, decode_steps: int = 4) -> dict:
+    """Config 4: a random-init Llama-3-8B-architecture model (lm_head bf16), `batch` sequences
+    prefilled to `context` tokens by the bf16 model, then `decode_steps` teacher-forced decode
+    steps with bf16 linears (the reference path) and with int8 W8A16 linears, from the same KV
+    state. Reports the per-step linear time of each stack (replayed from a captured graph at
+    M = batch), aggregate HBM GB/s, the greedy next-token match rate against the bf16 reference
+    (limited by quantization: random-init logits are nearly flat) and against an eager torch
+    restatement of the same int8 weights (the kernels' own parity), and the top-2 logit margin."""
+    import torch
+
+    from llm_serving_engine_amd.decode_step import DecodeRunner, random_llama
+
+    def note(msg: str) -> None:
+        print(f"[decode-step] {msg}", file=sys.stderr, flush=True)
+
+    model = random_llama(layers, seed=4000, device=dev)
+    note(f"model ready: {layers} layers")
+    runner = DecodeRunner(model, batch, context + decode_steps)
+    gen = torch.Generator().manual_seed(4001)
+    vocab = model.config.vocab_size
+    prompt = torch.randint(0, vocab, (batch, context), generator=gen).to(dev)
+    runner.prefill(prompt)
+    torch.cuda.synchronize()
+    note(f"prefilled {batch} x {context}")
+    tok = torch.randint(0, vocab, (batch,), generator=gen).to(dev)
+    inputs, ref_top, margins = [], [], []
+    for t in range(decode_steps):
+        inputs.append(tok)
+        logits = runner.step(tok, context + t).float()
+        top2 = logits.topk(2, dim=-1)
+        ref_top.append(top2.indices[:, 0])
+        margins.append((top2.values[:, 0] - top2.values[:, 1]) / logits.std(dim=-1))
+        tok = top2.indices[:, 0]
+    bf16_calls = runner.linear_calls(batch)
+    bf16_bytes = runner.linear_bytes(batch)
+    t_bf16 = time_graph(lambda: [mod(x) for mod, x in bf16_calls], steps)
+    note("bf16 steps and linear stack timed")
+    runner.quantize("int8")
+    runner.use("int8")
+    note("quantized")
+    match = match_torch = 0
+    rel = []
+    for t in range(decode_steps):
+        runner.use("int8-torch")
+        restated = runner.step(inputs[t], context + t).float()
+        runner.use("int8")
+        logits = runner.step(inputs[t], context + t).float()
+        rel.append(float((logits - restated).norm() / restated.norm()))
+        top = logits.argmax(-1)
+        match += int((top == ref_top[t]).sum())
+        match_torch += int((top == restated.argmax(-1)).sum())
+    int8_calls = runner.linear_calls(batch)
+    int8_bytes = runner.linear_bytes(batch)
+    t_int8 = time_graph(lambda: [mod(x) for mod, x in int8_calls], steps)
+    h = torch.randn(batch, model.config.hidden_size, generator=gen).to(torch.bfloat16).to(dev)
+    t_head = time_graph(lambda: model.lm_head(h), steps)
+    head_bytes = 2 * model.lm_head.weight.numel()
+    margin = torch.cat(margins)
+    return {
+        "layers": layers, "batch": batch, "context": context,
+        "int8_linear_us_per_step": round(t_int8 * 1e6, 1),
+        "int8_linear_gbps": round(int8_bytes / t_int8 / 1e9, 1),
+        "int8_linear_bytes": int8_bytes,
+        "bf16_linear_us_per_step": round(t_bf16 * 1e6, 1),
+        "bf16_linear_gbps": round(bf16_bytes / t_bf16 / 1e9, 1),
+        "lm_head_bf16_us": round(t_head * 1e6, 1),
+        "lm_head_gbps": round(head_bytes / t_head / 1e9, 1),
+        "greedy_match_rate": round(match / (batch * decode_steps), 4),
+        "greedy_match_rate_vs_int8_torch_restatement": round(
+            match_torch / (batch * decode_steps), 4),
+        "logit_rel_diff_vs_int8_torch_restatement": round(max(rel), 5),
+        "tokens_compared": batch * decode_steps,
+        "top2_margin_over_logit_std": {"median": round(float(margin.median()), 4),
+                                       "min": round(float(margin.min()), 5)},
+    }
+
+
 def main() -> None:
     args = parse()
     if args.summarize_profiles:
@@ -390,6 +481,9 @@ def main() -> None:
         return
     if args.only == "w8a8":
         print(json.dumps({"w8a8": bench_w8a8(pkg, dev, args.steps, gen)}))
+        return
+    if args.only == "decode-step":
+        print(json.dumps({"decode_step": bench_decode_step(pkg, dev, args.steps)}))
         return
 
     secondary = {}

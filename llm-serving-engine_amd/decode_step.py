@@ -1,0 +1,239 @@
+"""Config 4: the decode-step linear stack of a Llama-3-8B-architecture model, through a runner
+that follows the reference's fused decoder path.
+
+The reference's eager path flattens a batch plan into one (1, total_tokens) row of tokens and
+runs `decoder_hidden` (src/llm_serving_engine/model/model_runner.py:213-224): embedding, rotary
+embedding, then per layer `hidden += attend(input_layernorm(hidden))` and
+`hidden += mlp(post_attention_layernorm(hidden))`, then the final norm; `emit_owed`
+(model_runner.py:290-308) applies the bf16 lm_head to each sequence's last row and greedy
+sampling takes the argmax (sampling.py:34-36). Its attention projects q/k/v with three
+`nn.Linear` calls and rotates q and k (`_project_qkv`, model_runner.py:310-326), attends, then
+applies o_proj (`attention_output`, model_runner.py:365-369).
+
+`DecodeRunner` runs exactly that sequence over HF Llama modules, with two linear back ends:
+  * "bf16": the reference's own `nn.Linear` modules (q, k, v, o, gate, up, down: seven GEMMs a
+    layer on the vendor BLAS);
+  * "int8" / "w8a8": `Int8Linear` on the fused shapes the kernels are tuned for (one (4096, 6144)
+    QKV projection and one (4096, 28672) gate_up projection, split after the GEMM), o_proj and
+    down_proj. Per-channel quantization of a row-stacked weight equals quantizing each part;
+  * "int8-torch": the same quantized weights, applied by an eager torch restatement of W8A16
+    (x and q·s in fp32, one fp32 matmul, bf16 out) instead of the HIP kernels; it isolates the
+    kernels from the quantization itself. Test and measurement use only.
+lm_head stays bf16 in both. Attention runs in fp32 over a contiguous per-layer KV cache (the
+reference's `contiguous_attention` path, model_runner.py:400-418), so both back ends see the
+same attention arithmetic and only the linears differ.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import nn
+
+from .int8_linear import Int8Linear
+
+LLAMA3_8B = dict(
+    hidden_size=4096,
+    intermediate_size=14336,
+    num_attention_heads=32,
+    num_key_value_heads=8,
+    head_dim=128,
+    vocab_size=128256,
+    rope_theta=500000.0,
+    rms_norm_eps=1e-5,
+    max_position_embeddings=8192,
+    initializer_range=0.02,
+)
+
+
+def random_llama(num_layers: int, seed: int, device: torch.device, **overrides) -> nn.Module:
+    """A random-init Llama-3-8B-architecture `LlamaForCausalLM` in bf16 on `device` (weights
+    ~ N(0, 0.02), the architecture's own initializer_range; there is no checkpoint offline)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(**{**LLAMA3_8B, **overrides, "num_hidden_layers": num_layers})
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = LlamaForCausalLM._from_config(cfg, dtype=torch.bfloat16)
+    model.eval()
+    return model
+
+
+class DecodeRunner:
+    """Decode steps of `batch` sequences, one token each, over a contiguous KV cache of
+    `capacity` positions per sequence."""
+
+    def __init__(self, model: nn.Module, batch: int, capacity: int) -> None:
+        self.model = model
+        cfg = model.config
+        self.layers = list(model.model.layers)
+        self.batch = batch
+        self.capacity = capacity
+        self.n_heads = cfg.num_attention_heads
+        self.n_kv = cfg.num_key_value_heads
+        self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // self.n_heads
+        dev = next(model.parameters()).device
+        shape = (batch, self.n_kv, capacity, self.head_dim)
+        self.k_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
+        self.v_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
+        self.int8: list[dict[str, Int8Linear]] | None = None
+        self.backend = "bf16"
+
+    # ---- linear back ends ---------------------------------------------------------------------
+
+    @torch.no_grad()
+    def quantize(self, mode: str = "int8") -> None:
+        """Builds the int8 projections from the bf16 weights (kept, for the bf16 back end)."""
+        self.int8 = []
+        for layer in self.layers:
+            attn, mlp = layer.self_attn, layer.mlp
+            qkv = torch.cat([attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight])
+            gate_up = torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight])
+            self.int8.append({
+                "qkv": _int8(qkv, mode),
+                "o": _int8(attn.o_proj.weight, mode),
+                "gate_up": _int8(gate_up, mode),
+                "down": _int8(mlp.down_proj.weight, mode),
+            })
+            del qkv, gate_up
+        torch.cuda.empty_cache()
+
+    def use(self, backend: str) -> None:
+        if backend not in ("bf16", "int8", "int8-torch"):
+            raise ValueError(f"unknown back end {backend!r}")
+        if backend != "bf16" and self.int8 is None:
+            raise RuntimeError("quantize() first")
+        self.backend = backend
+
+    def _lin(self, i: int, name: str, x: torch.Tensor) -> torch.Tensor:
+        mod = self.int8[i][name]
+        if self.backend == "int8":
+            return mod(x)
+        w = mod.unpacked_qweight().float() * mod.scales[:, None]
+        return (x.float() @ w.t()).to(torch.bfloat16)
+
+    def _qkv(self, i: int, normed: torch.Tensor):
+        if self.backend == "bf16":
+            attn = self.layers[i].self_attn
+            return attn.q_proj(normed), attn.k_proj(normed), attn.v_proj(normed)
+        qkv = self._lin(i, "qkv", normed)
+        nq, nkv = self.n_heads * self.head_dim, self.n_kv * self.head_dim
+        return qkv[..., :nq], qkv[..., nq:nq + nkv], qkv[..., nq + nkv:]
+
+    def _o(self, i: int, x: torch.Tensor) -> torch.Tensor:
+        if self.backend == "bf16":
+            return self.layers[i].self_attn.o_proj(x)
+        return self._lin(i, "o", x)
+
+    def _mlp(self, i: int, x: torch.Tensor) -> torch.Tensor:
+        mlp = self.layers[i].mlp
+        if self.backend == "bf16":
+            return mlp(x)
+        gu = self._lin(i, "gate_up", x)
+        inter = gu.shape[-1] // 2
+        return self._lin(i, "down", mlp.act_fn(gu[..., :inter]) * gu[..., inter:])
+
+    # ---- the step -----------------------------------------------------------------------------
+
+    def _attend(self, i: int, normed: torch.Tensor, rope, pos: torch.Tensor, nseq: int,
+                ntok: int) -> torch.Tensor:
+        """normed (1, nseq*ntok, hidden), sequences contiguous, positions pos (nseq, ntok) equal
+        across sequences. Writes K/V at those positions and attends causally over [0, end)."""
+        from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+        q, k, v = self._qkv(i, normed)
+        q = q.reshape(nseq, ntok, self.n_heads, self.head_dim).transpose(1, 2)
+        k = k.reshape(nseq, ntok, self.n_kv, self.head_dim).transpose(1, 2)
+        v = v.reshape(nseq, ntok, self.n_kv, self.head_dim).transpose(1, 2)
+        cos, sin = rope
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        start = int(pos[0, 0])
+        end = start + ntok
+        self.k_cache[i][self._rows, :, start:end] = k
+        self.v_cache[i][self._rows, :, start:end] = v
+        keys = self.k_cache[i][self._rows, :, :end].float()
+        vals = self.v_cache[i][self._rows, :, :end].float()
+        rep = self.n_heads // self.n_kv
+        keys = keys.repeat_interleave(rep, dim=1)
+        vals = vals.repeat_interleave(rep, dim=1)
+        scores = torch.matmul(q.float(), keys.transpose(-1, -2).contiguous())
+        scores = scores / math.sqrt(self.head_dim)
+        qpos = torch.arange(start, end, device=scores.device)[:, None]
+        kpos = torch.arange(end, device=scores.device)[None, :]
+        scores = scores.masked_fill(kpos > qpos, float("-inf"))
+        out = torch.matmul(torch.softmax(scores, dim=-1), vals)
+        out = out.to(torch.bfloat16).transpose(1, 2).reshape(1, nseq * ntok, -1)
+        return self._o(i, out)
+
+    @torch.no_grad()
+    def forward(self, tokens: torch.Tensor, start: int, rows: slice | None = None) -> torch.Tensor:
+        """tokens (nseq, ntok) of sequences `rows` (default: all) at positions [start,
+        start + ntok) -> final-norm hidden of every token, (1, nseq*ntok, hidden)."""
+        self._rows = rows if rows is not None else slice(None)
+        nseq, ntok = tokens.shape
+        model = self.model.model
+        ids = tokens.reshape(1, nseq * ntok)
+        pos = torch.arange(start, start + ntok, device=tokens.device).repeat(nseq, 1)
+        hidden = model.embed_tokens(ids)
+        cos, sin = model.rotary_emb(hidden, pos.reshape(1, -1))
+        rope = (cos.reshape(nseq, ntok, -1), sin.reshape(nseq, ntok, -1))
+        for i, layer in enumerate(self.layers):
+            hidden = hidden + self._attend(i, layer.input_layernorm(hidden), rope, pos, nseq, ntok)
+            hidden = hidden + self._mlp(i, layer.post_attention_layernorm(hidden))
+        return model.norm(hidden)
+
+    @torch.no_grad()
+    def prefill(self, tokens: torch.Tensor, chunk: int = 8) -> None:
+        """Fills positions [0, tokens.shape[1]) of every sequence's cache, `chunk` sequences at a
+        time."""
+        for s in range(0, tokens.shape[0], chunk):
+            self.forward(tokens[s:s + chunk], 0, slice(s, s + chunk))
+
+    @torch.no_grad()
+    def step(self, tokens: torch.Tensor, position: int) -> torch.Tensor:
+        """One decode step: tokens (batch,) at `position` -> bf16 logits (batch, vocab) from the
+        bf16 lm_head (the reference's emit_owed)."""
+        hidden = self.forward(tokens[:, None], position)
+        return self.model.lm_head(hidden[0])
+
+    # ---- linear-only timing -------------------------------------------------------------------
+
+    def linear_calls(self, m: int) -> list:
+        """(module, input) for every projection of one decode step at M = m, with inputs of the
+        right shapes (the values do not change the time of a weight stream)."""
+        dev = next(self.model.parameters()).device
+        g = torch.Generator(device="cpu").manual_seed(7)
+        hid = self.model.config.hidden_size
+        inter = self.model.config.intermediate_size
+        x_h = torch.randn(m, hid, generator=g).to(torch.bfloat16).to(dev)
+        x_i = torch.randn(m, inter, generator=g).to(torch.bfloat16).to(dev)
+        calls = []
+        for i, layer in enumerate(self.layers):
+            if self.backend == "bf16":
+                a, p = layer.self_attn, layer.mlp
+                calls += [(a.q_proj, x_h), (a.k_proj, x_h), (a.v_proj, x_h), (a.o_proj, x_h),
+                          (p.gate_proj, x_h), (p.up_proj, x_h), (p.down_proj, x_i)]
+            else:
+                d = self.int8[i]
+                calls += [(d["qkv"], x_h), (d["o"], x_h), (d["gate_up"], x_h), (d["down"], x_i)]
+        return calls
+
+    def linear_bytes(self, m: int) -> int:
+        """Algorithmic bytes of the step's projections (weights, scales, activations in and
+        out), excluding lm_head."""
+        total = 0
+        for mod, x in self.linear_calls(m):
+            k, n = x.shape[-1], mod.out_features
+            if isinstance(mod, Int8Linear):
+                total += k * n + 4 * n + 2 * m * k + 2 * m * n
+            else:
+                total += 2 * k * n + 2 * m * k + 2 * m * n
+        return total
+
+
+def _int8(weight: torch.Tensor, mode: str) -> Int8Linear:
+    lin = nn.Linear(weight.shape[1], weight.shape[0], bias=False, device=weight.device,
+                    dtype=weight.dtype)
+    lin.weight.data = weight
+    return Int8Linear.from_linear(lin, mode)
