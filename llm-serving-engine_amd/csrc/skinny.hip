@@ -72,6 +72,16 @@ struct SkinnyWStage {
   uint4 w[RT];
 };
 
+// XOR swizzle of a streamed activation step image (16 MT token rows of XROW = 64 ESZ bytes,
+// 16-byte chunks): chunk c of row m sits at c ^ xstep_swz(m). A fragment read takes one logical
+// chunk of 16 consecutive rows; rows are 128 (bf16) or 64 (int8) bytes, so 2 or 4 consecutive
+// rows share a 256-byte bank line, and the swizzle varies with m >> 1 (m >> 2) to give those 16
+// rows 16 distinct bank groups.
+template <int ESZ>
+__host__ __device__ constexpr int xstep_swz(int m) {
+  return ESZ == 2 ? (m >> 1) & 7 : (m >> 2) & 3;
+}
+
 // Bytes of one whole-staged activation row: K rounded up to whole 64-wide steps.
 __host__ __device__ constexpr int skinny_x_row(int K, int esz) { return ((K + 63) / 64) * 64 * esz; }
 
@@ -97,7 +107,7 @@ skinny_kernel(SkinnyArgs a) {
   static_assert(DW % DX == 0, "the activation ring index must repeat with the weight ring's");
   // Streamed activations: a wave's ring slot holds the 16 MT token rows x 64 K-columns of one of
   // its steps, row-major (XROW bytes a row), 16-byte chunks XOR-swizzled by token (chunk c of row
-  // m sits at c ^ (m % XCH)); the wave fills it with XI pieces of 1 KB.
+  // m sits at c ^ xstep_swz(m)); the wave fills it with XI pieces of 1 KB.
   constexpr int XROW = 64 * ESZ;                // bytes of one token row of a step
   constexpr int XCH = XROW / 16;                // chunks per row
   constexpr int XI = XLDS ? 0 : MT * ESZ;       // 1 KB pieces per wave per step
@@ -207,7 +217,7 @@ skinny_kernel(SkinnyArgs a) {
   };
   // Activation load cursor (activations depend on the step only, not on the panel). Piece i of
   // this wave's part of a slot covers bytes [1024 i, 1024 i + 1024): lane l fills byte
-  // 1024 i + 16 l, physical chunk pc of token row m, which holds logical chunk pc ^ (m % XCH).
+  // 1024 i + 16 l, physical chunk pc of token row m, which holds logical chunk pc ^ xstep_swz(m).
   // Tokens past M, K past the end and steps past the range read zeros.
   int xu = u_first, xp = u_first % a.panels, xsp = u_first / a.panels, xsu = 0;
   auto load_x = [&](int slot) {
@@ -218,7 +228,7 @@ skinny_kernel(SkinnyArgs a) {
     for (int i = 0; i < XI; ++i) {
       const int o = 1024 * i + 16 * lane;
       const int m = o / XROW, pc = (o % XROW) / 16;
-      const int kb = XROW * j + 16 * (pc ^ (m & (XCH - 1)));
+      const int kb = XROW * j + 16 * (pc ^ xstep_swz<ESZ>(m));
       const uint32_t off = live && m < a.M && kb < a.K * ESZ
                                ? (uint32_t)((int64_t)m * a.ldx * ESZ + kb)
                                : kOutOfRange;
@@ -273,7 +283,7 @@ skinny_kernel(SkinnyArgs a) {
         for (int h = 0; h < XL; ++h) {
           // Lane group g takes 16 consecutive K elements of the step: XL chunks of 16 bytes.
           const int c = XL * g + h;
-          xv[b][h] = *reinterpret_cast<const uint4*>(base + m * XROW + 16 * (c ^ (m & (XCH - 1))));
+          xv[b][h] = *reinterpret_cast<const uint4*>(base + m * XROW + 16 * (c ^ xstep_swz<ESZ>(m)));
         }
       }
     }
