@@ -49,6 +49,8 @@ LAYERS = 8
 CALIBRATION_BYTES = 64 << 20
 PROFILE_MD = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.md"
 PROFILE_TRAFFIC = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.traffic.json"
+PROFILE_PREFILL = REPO_ROOT / "profiles" / "tiled_gemm_kernel_prefill.md"
+CUS, SIMDS_PER_CU, XCDS = 256, 4, 8
 
 
 def decode_bytes(m: int, k: int, n: int) -> int:
@@ -66,6 +68,8 @@ def parse() -> argparse.Namespace:
                    help="one family; decode-step is config 4 (a 32-layer model's decode step)")
     p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
                    help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
+    p.add_argument("--summarize-prefill", nargs=2, metavar=("TRACE", "PMC"),
+                   help="summarize rocprofv3 output dirs of --only prefill into profiles/")
     return p.parse_args()
 
 
@@ -352,6 +356,89 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> None:
     print("\n".join(out))
 
 
+def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
+    """Per (M, shape) duration, TFLOP/s and MFMA utilisation of the tiled kernel from a kernel
+    trace and a counter run of `bench.py --only prefill` (each M runs a warmup step and the timed
+    steps, each step the four shapes in order)."""
+    import csv
+    import statistics
+
+    def read(path):
+        with open(path, newline="") as f:
+            return list(csv.DictReader(f))
+
+    trace = sorted((r for r in read(Path(trace_dir) / "run_kernel_trace.csv")
+                    if "tiled_gemm_kernel" in r["Kernel_Name"]),
+                   key=lambda r: int(r["Start_Timestamp"]))
+    pmc = collections_by_dispatch(read(Path(pmc_dir) / "run_counter_collection.csv"),
+                                  "tiled_gemm_kernel")
+    per_m = len(trace) // len(PREFILL_MS)
+    rows = []
+    for mi, m in enumerate(PREFILL_MS):
+        block = trace[mi * per_m:(mi + 1) * per_m]
+        pblock = pmc[mi * per_m:(mi + 1) * per_m]
+        for si, (k, n) in enumerate(SHAPES):
+            ds = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                  for r in block[si::len(SHAPES)]]
+            us = statistics.median(ds)
+            counters = pblock[si::len(SHAPES)]
+            busy = statistics.median(c["SQ_VALU_MFMA_BUSY_CYCLES"] for c in counters)
+            active = statistics.median(c["GRBM_GUI_ACTIVE"] for c in counters)
+            insts = statistics.median(c["SQ_INSTS_MFMA"] for c in counters)
+            flops = 2.0 * m * n * k
+            name = block[si]["Kernel_Name"].split("(")[0].replace("void lse::", "")
+            # GRBM_GUI_ACTIVE comes summed over the XCDs: per XCD it is the kernel's length in
+            # engine clocks, which gives the clock the kernel actually ran at.
+            cycles = active / XCDS
+            rows.append((m, SHAPE_NAMES[si], k, n, name, us, flops / us / 1e6, insts, busy,
+                         cycles / us / 1e3, busy / (CUS * SIMDS_PER_CU * cycles)))
+    cmds = [
+        "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_prefill -o run --output-format csv "
+        "-- python3 bench.py --only prefill --steps 8",
+        "rocprofv3 --pmc SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE -d "
+        "gpurun_out/pmc_prefill -o run --output-format csv -- python3 bench.py --only prefill "
+        "--steps 8",
+        "python3 bench.py --summarize-prefill gpurun_out/prof_prefill gpurun_out/pmc_prefill",
+    ]
+    out = ["# tiled_gemm_kernel — config-2 W8A16 prefill (Llama-3-8B shapes, M in "
+           f"{PREFILL_MS}), one MI355X", "",
+           "Commands (repository root, one MI355X; the last runs on any host):", "", "```", *cmds,
+           "```", "",
+           "frac of 2.5 PF: achieved TFLOP/s (2MNK over the kernel-trace duration) over the "
+           "dense bf16 peak. Each v_mfma_f32_16x16x32_bf16 keeps a SIMD's matrix core busy 16 "
+           "cycles (SQ_INSTS_MFMA x 16 = SQ_VALU_MFMA_BUSY_CYCLES below); 256 CUs x 4 SIMDs at "
+           "2.4 GHz is the 2.5 PFLOP/s peak. GRBM_GUI_ACTIVE, reported summed over the 8 XCDs, "
+           "gives the kernel's length in engine clocks, hence the clock it ran at; MFMA "
+           "utilisation = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x those clocks) is the fraction "
+           "of matrix-core cycles used at that clock. For kernels under ~100 us the GRBM window "
+           "also spans launch overhead (implied clocks above 2.4 GHz), so read those two columns "
+           "for the long kernels: under sustained MFMA load the chip holds ~1.8-1.9 GHz, "
+           "i.e. ~1.9 PFLOP/s of reachable dense bf16.", "",
+           "| M | shape (K,N) | kernel | us | TFLOP/s | frac of 2.5 PF | MFMA instrs | MFMA busy "
+           "cycles | clock (GHz) | MFMA utilisation |", "|---|---|---|---|---|---|---|---|---|---|"]
+    tot_f = tot_t = 0.0
+    for m, sn, k, n, name, us, tf, insts, busy, ghz, util in rows:
+        out.append(f"| {m} | {sn} ({k},{n}) | `{name}` | {us:.1f} | {tf:.0f} | {tf / 2500:.3f} | "
+                   f"{insts:,.0f} | {busy:,.0f} | {ghz:.2f} | {util:.3f} |")
+        if m == 2048:
+            tot_f += 2.0 * m * n * k
+            tot_t += us
+    out += ["", f"M = 2048, four shapes: {tot_f / 1e9:.0f} GFLOP in {tot_t:.1f} us -> "
+            f"{tot_f / tot_t / 1e6:.0f} TFLOP/s ({tot_f / tot_t / 1e6 / 2500:.3f} of 2.5 PFLOP/s)."]
+    PROFILE_PREFILL.write_text("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
+def collections_by_dispatch(rows: list[dict], kernel: str) -> list[dict]:
+    """Counter rows of one --pmc run -> one {counter: value} dict per dispatch of `kernel`, in
+    dispatch order."""
+    by: dict[int, dict] = {}
+    for r in rows:
+        if kernel in r["Kernel_Name"]:
+            by.setdefault(int(r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+    return [by[d] for d in sorted(by)]
+
+
 def measured_traffic(dec: dict) -> float | None:
     """HBM bytes per decode call from the committed PMC summary of this same sweep, or None."""
     try:
@@ -457,6 +544,9 @@ def main() -> None:
     args = parse()
     if args.summarize_profiles:
         summarize_profiles(*args.summarize_profiles)
+        return
+    if args.summarize_prefill:
+        summarize_prefill(*args.summarize_prefill)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the int8 Linear "
