@@ -97,7 +97,6 @@ __global__ void __launch_bounds__(64 * W)
 skinny_kernel(SkinnyArgs a) {
   using Acc = std::conditional_t<I8, i32x4, f32x4>;
   constexpr int SLICES = RT * MT;               // 16x16 output tiles of a panel
-  constexpr int SPW = (SLICES + W - 1) / W;     // epilogue slices per wave
   constexpr int ESZ = I8 ? 1 : 2;               // activation element bytes
   constexpr int XL = I8 ? 1 : 2;                // 16-byte activation pieces per token tile and step
   // A single accumulator chain in W8A16 splits into two (one per dequantized half), so the two
@@ -113,15 +112,21 @@ skinny_kernel(SkinnyArgs a) {
   constexpr int XI = XLDS ? 0 : MT * ESZ;       // 1 KB pieces per wave per step
   constexpr int kWaitX = (DX - 1) * (RT + XI);  // loads issued after a step's activations
   static_assert(XLDS || kWaitX < 64, "vmcnt holds at most 63");
-  constexpr int RSLOTS = W < SLICES ? W : SLICES;  // slices reduced per pass through LDS
-
-  __shared__ Acc red[W][RSLOTS][64];
-  __shared__ float s_lds[kSkinnyScaleLds];
   // Each ring slot (all waves' parts) is its own array, so the compiler can tell the slot a
   // direct-to-LDS load fills from the slot the MFMAs read, and leaves those waits to the explicit
   // s_waitcnt.
   constexpr int XWAVE = 16 * MT * XROW / 16;    // uint4 per wave per slot
   constexpr int XSLOT = XLDS ? 1 : W * XWAVE;
+  // Slices reduced per pass through LDS: all W waves' partials of RS slices (1 KB each) at once,
+  // as many as the LDS left by the activation ring and the scales holds.
+  constexpr int kRedBudget = 160 * 1024 - DX * XSLOT * 16 - kSkinnyScaleLds * 4;
+  constexpr int RS0 = W < SLICES ? W : SLICES;
+  constexpr int RS = RS0 * W * 1024 <= kRedBudget ? RS0 : kRedBudget / (W * 1024);
+  static_assert(RS >= 1, "no LDS left for the cross-wave reduction");
+  constexpr int NPASS = (SLICES + RS - 1) / RS;
+
+  __shared__ Acc red[W][RS][64];
+  __shared__ float s_lds[kSkinnyScaleLds];
   __shared__ uint4 xs0[XSLOT], xs1[DX > 1 ? XSLOT : 1], xs2[DX > 2 ? XSLOT : 1],
       xs3[DX > 3 ? XSLOT : 1];
   static_assert(XLDS || DX <= 4, "at most four activation slots");
@@ -332,25 +337,25 @@ skinny_kernel(SkinnyArgs a) {
     store_out4<I8>(a.y, a.ldy, a.acc, a.N, m, n, cnt, v, sc, sxv[b], yvec);
   };
 
-  // End of a unit (panel p of split sp): pass i adds slices [i W, i W + RSLOTS) over the waves in
-  // wave order; wave w keeps slice i W + w and stores it.
+  // End of a unit (panel p of split sp): pass i adds slices [i RS, i RS + RS) over the waves in
+  // wave order; wave w < RS keeps slice i RS + w and stores it.
   auto unit_end = [&](int p, int sp) {
 #pragma unroll
-    for (int i = 0; i < SPW; ++i) {
+    for (int i = 0; i < NPASS; ++i) {
       __syncthreads();  // the previous pass's (or panel's) reads of red are done
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int b = 0; b < MT; ++b) {
-          const int sl = rt + RT * b - W * i;
-          if (sl < 0 || sl >= RSLOTS) continue;
+          const int sl = rt + RT * b - RS * i;
+          if (sl < 0 || sl >= RS) continue;
           Acc v = acc[rt][b][0];
           if constexpr (NACC == 2) v += acc[rt][b][1];
           red[wave][sl][lane] = v;
         }
       __syncthreads();
-      const int slice = wave + W * i;
-      if (slice < SLICES) {
+      const int slice = wave + RS * i;
+      if (wave < RS && slice < SLICES) {
         Acc v = red[0][wave][lane];
 #pragma unroll
         for (int w2 = 1; w2 < W; ++w2) v += red[w2][wave][lane];
@@ -423,7 +428,7 @@ skinny_reduce(SkinnyArgs a) {
 // ---- host side -----------------------------------------------------------------------------
 
 // Kernel configuration: token tiles MT (the class of M), row tiles per panel RT, waves W, ring
-// depths, K splits S. MT, RT, W and S fix every summation order, so they depend on the class, N,
+// depths, K splits S (measured per class and shape on MI355X). MT, RT, W and S fix every summation order, so they depend on the class, N,
 // K and the CU count only, never on M inside a class. Staged (XLDS) and streamed activations feed
 // the same MFMAs in the same order, so the choice between them (by M and K) changes no result.
 struct SkinnyShape {
@@ -463,7 +468,9 @@ static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K) {
   if (skinny_split_k(N, K)) return {mt, 4, 4, 4, false, 4};
   const int rt = skinny_rt(N);
   if (mt == 2) return {2, rt, rt == 4 ? 4 : 8, 4, false, 1};
-  return {4, rt, 4, 4, false, 1};
+  // 64 tokens: two waves per SIMD (eight per workgroup, shallower rings) for 32- and 64-row
+  // panels, one per SIMD with a deeper ring for single row tiles.
+  return rt == 1 ? SkinnyShape{4, 1, 4, 4, false, 1} : SkinnyShape{4, rt, 8, 2, false, 1};
 }
 
 template <bool I8>
@@ -477,7 +484,8 @@ static const void* skinny_kernel_for(const SkinnyShape& sh) {
     return skinny_fn<I8, 2, 4, 4, 4, 4, false>();
   }
   if (sh.rt == 1) return skinny_fn<I8, 4, 1, 4, 4, 4, false>();
-  if (sh.rt == 2) return skinny_fn<I8, 4, 2, 4, 4, 4, false>();
+  if (sh.rt == 2) return skinny_fn<I8, 4, 2, 8, 2, 2, false>();
+  if (sh.w == 8) return skinny_fn<I8, 4, 4, 8, 2, 2, false>();
   return skinny_fn<I8, 4, 4, 4, 4, 2, false>();
 }
 
