@@ -76,7 +76,7 @@ enum lse_query_key {
   LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
 };
 
-#define LSE_ABI_VERSION 3
+#define LSE_ABI_VERSION 4
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -157,6 +157,45 @@ int lse_quantize_act_per_token(const void* x, int64_t ldx, int8_t* xq, float* sx
 int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* y,
                   int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* workspace,
                   int64_t workspace_bytes, void* stream);
+
+/* Bytes of the packed gate/up layout of two (I, K) weights: 2 * ceil(I/16) * ceil(K/64) * 1024. */
+int64_t lse_packed_glu_bytes(int64_t I, int64_t K);
+
+/*
+ * Packs the MLP's stacked gate/up weight, row-major (2I, K) int8 = [gate rows 0..I-1; up rows
+ * 0..I-1] (contiguous, K % LSE_K_ALIGN == 0, 16-byte aligned), into the gate/up layout the GLU
+ * entry points read (qp: lse_packed_glu_bytes(I, K) bytes, 16-byte aligned): packed row tile 2t
+ * is the lse_pack_weight tile of gate rows 16t..16t+15, row tile 2t+1 that of the same up rows,
+ * zero past I. Load time only.
+ * Replaces: the separate `gate_proj.weight` and `up_proj.weight` of `LlamaMLP`
+ * (modeling_llama.py:169-170) at the int8 switch (model_runner.py:45-46).
+ */
+int lse_pack_glu(const int8_t* q, int64_t I, int64_t K, int8_t* qp, void* stream);
+
+/*
+ * Fused gate/up projection and SiLU-mul, W8A16. For n < I, in fp32:
+ *   g = s[n] * sum_k x[m,k] q[n,k],   u = s[I+n] * sum_k x[m,k] q[I+n,k],
+ *   h[m,n] = bf16_rne(silu(g) * u),   silu(v) = v / (1 + e^-v),
+ * q being the stacked (2I, K) weight given packed by lse_pack_glu and s its (2I) fp32 scales
+ * [gate; up]. x as for lse_w8a16_gemm (K % LSE_K_ALIGN == 0). h: (M, I) bf16, row stride
+ * ldh >= I. algo: enum lse_algo, as for lse_w8a16_gemm_algo. Needs no workspace.
+ * Replaces: `self.act_fn(self.gate_proj(x)) * self.up_proj(x)` in `LlamaMLP.forward`
+ * (modeling_llama.py:175, reached from decoder_hidden, model_runner.py:223): two GEMMs, the
+ * activation and the product, each rounding to bf16, become one kernel that rounds once.
+ */
+int lse_w8a16_glu(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* h,
+                  int64_t ldh, int64_t M, int64_t I, int64_t K, int algo, void* stream);
+
+/*
+ * Fused gate/up projection and SiLU-mul, W8A8: with xq, sx from lse_quantize_act_per_token and
+ * acc_g, acc_u the exact int32 sums of gate row n and up row n,
+ *   g = (fp32(acc_g) * sx[m]) * s[n],   u = (fp32(acc_u) * sx[m]) * s[I+n],
+ *   h[m,n] = bf16_rne(silu(g) * u).
+ * Operands as for lse_w8a8_gemm (K <= LSE_MAX_K) and lse_w8a16_glu. Needs no workspace.
+ * Replaces: the same LlamaMLP expression (modeling_llama.py:175) in the dynamic per-token mode.
+ */
+int lse_w8a8_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* h,
+                 int64_t ldh, int64_t M, int64_t I, int64_t K, void* stream);
 
 /* Static properties (enum lse_query_key); -1 for an unknown key. Load-time checks read these,
  * as `ModelRunner.check_custom_kernel_support` (model_runner.py:77-94) checks its kernels. */

@@ -7,11 +7,13 @@ it as `llm_serving_engine_amd`.
 from . import ops
 from ._lib import LIB_PATH, library
 from .config import ModelConfig
-from .int8_linear import Int8Linear, check_linear_supported
+from .int8_linear import Int8GateUp, Int8GluMLP, Int8Linear, check_linear_supported
 from .quantize import check_int8_support, quantize_model_
 
 __all__ = [
     "LIB_PATH",
+    "Int8GateUp",
+    "Int8GluMLP",
     "Int8Linear",
     "ModelConfig",
     "check_int8_support",

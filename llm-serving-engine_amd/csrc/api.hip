@@ -13,7 +13,9 @@ int launch_quantize_weight(const float* w, int64_t ldw, int8_t* q, float* s, int
 int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, int64_t M,
                         int64_t K, hipStream_t stream);
 int launch_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, hipStream_t stream);
+int launch_pack_glu(const int8_t* q, int64_t I, int64_t K, int8_t* qp, hipStream_t stream);
 int64_t packed_weight_bytes(int64_t N, int64_t K);
+int64_t packed_glu_bytes(int64_t I, int64_t K);
 int64_t skinny_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K);
 int launch_w8a16_skinny(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
                         uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
@@ -26,6 +28,18 @@ int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* q, const flo
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s,
                      uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
                      hipStream_t stream);
+int launch_w8a16_skinny_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                            uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                            hipStream_t stream);
+int launch_w8a8_skinny_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                           uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                           hipStream_t stream);
+int launch_w8a16_gemm_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                          uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                          hipStream_t stream);
+int launch_w8a8_gemm_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                         uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                         hipStream_t stream);
 }  // namespace lse
 
 namespace lse {
@@ -111,6 +125,10 @@ int check_packed(int64_t N, int64_t K) {
   return lse::packed_weight_bytes(N, K) < (int64_t)kBufferLimit ? LSE_OK : LSE_E_RANGE;
 }
 
+int check_packed_glu(int64_t I, int64_t K) {
+  return lse::packed_glu_bytes(I, K) < (int64_t)kBufferLimit ? LSE_OK : LSE_E_RANGE;
+}
+
 }  // namespace
 
 extern "C" {
@@ -150,6 +168,21 @@ int lse_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, void* str
   if (!aligned(q, 16) || !aligned(qp, 16)) return LSE_E_ALIGN;
   if (int st = check_packed(N, K)) return st;
   return lse::launch_pack_weight(q, N, K, qp, (hipStream_t)stream);
+}
+
+int64_t lse_packed_glu_bytes(int64_t I, int64_t K) {
+  if (I < 0 || K < 0) return -1;
+  return lse::packed_glu_bytes(I, K);
+}
+
+int lse_pack_glu(const int8_t* q, int64_t I, int64_t K, int8_t* qp, void* stream) {
+  if (I < 0 || K < 0 || 2 * I > kMaxRows) return LSE_E_SHAPE;
+  if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
+  if (I == 0 || K == 0) return LSE_OK;
+  if (!q || !qp) return LSE_E_NULL;
+  if (!aligned(q, 16) || !aligned(qp, 16)) return LSE_E_ALIGN;
+  if (int st = check_packed_glu(I, K)) return st;
+  return lse::launch_pack_glu(q, I, K, qp, (hipStream_t)stream);
 }
 
 int64_t lse_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
@@ -223,6 +256,49 @@ int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const flo
   }
   if (256 * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
   return lse::launch_w8a8_gemm(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, st);
+}
+
+int lse_w8a16_glu(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* h,
+                  int64_t ldh, int64_t M, int64_t I, int64_t K, int algo, void* stream) {
+  if (I < 0 || 2 * I > kMaxRows) return LSE_E_SHAPE;
+  if (int st = check_common(qp, s, M, 2 * I, K)) return st;
+  if (algo < LSE_ALGO_AUTO || algo > LSE_ALGO_PREFILL) return LSE_E_ALGO;
+  if (algo == LSE_ALGO_DECODE && M > LSE_DECODE_MAX_M) return LSE_E_ALGO;
+  if (M == 0 || I == 0) return LSE_OK;
+  if (int st = check_bf16_matrix(h, ldh, M, I, 1)) return st;
+  hipStream_t st = (hipStream_t)stream;
+  if (K == 0) return zero_output(h, ldh, M, I, st);  // silu(0) * 0
+  if (int e = check_bf16_matrix(x, ldx, M, K, 8)) return e;
+  if (int e = check_packed_glu(I, K)) return e;
+  if (algo == LSE_ALGO_AUTO) algo = M <= LSE_DECODE_MAX_M ? LSE_ALGO_DECODE : LSE_ALGO_PREFILL;
+  if (algo == LSE_ALGO_DECODE) {
+    if (((M - 1) * ldx + K) * 2 >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+    return lse::launch_w8a16_skinny_glu((const uint16_t*)x, ldx, qp, s, (uint16_t*)h, ldh, M, I,
+                                        K, st);
+  }
+  if (256 * ldx * 2 >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+  return lse::launch_w8a16_gemm_glu((const uint16_t*)x, ldx, qp, s, (uint16_t*)h, ldh, M, I, K,
+                                    st);
+}
+
+int lse_w8a8_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* h,
+                 int64_t ldh, int64_t M, int64_t I, int64_t K, void* stream) {
+  if (I < 0 || 2 * I > kMaxRows) return LSE_E_SHAPE;
+  if (int st = check_common(qp, s, M, 2 * I, K)) return st;
+  if (M == 0 || I == 0) return LSE_OK;
+  if (!sx) return LSE_E_NULL;
+  if (int st = check_bf16_matrix(h, ldh, M, I, 1)) return st;
+  hipStream_t st = (hipStream_t)stream;
+  if (K == 0) return zero_output(h, ldh, M, I, st);
+  if (!xq) return LSE_E_NULL;
+  if (!aligned(xq, 16)) return LSE_E_ALIGN;
+  if (int e = check_packed_glu(I, K)) return e;
+  if (M <= LSE_DECODE_MAX_M) {
+    if (M * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+    return lse::launch_w8a8_skinny_glu(xq, sx, qp, s, (uint16_t*)h, ldh, M, I, K, st);
+  }
+  if (256 * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+  return lse::launch_w8a8_gemm_glu(xq, sx, qp, s, (uint16_t*)h, ldh, M, I, K, st);
 }
 
 int64_t lse_query(int key) {

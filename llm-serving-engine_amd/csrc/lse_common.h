@@ -83,11 +83,35 @@ __device__ __forceinline__ i32x4 mfma_i8(uint4 a, uint4 b, i32x4 c) {
 // byte 16 * l + i holds q[16 * rb + l % 16][64 * j + 16 * (l / 16) + i] (zero past N or K). One
 // 128-bit load per lane of a wave reads one whole tile, already in MFMA operand order: lane l
 // holds 16 K-consecutive bytes of row l % 16.
+//
+// Gate/up layout of the MLP's fused projection (two (I, K) matrices): row tile 2t holds gate rows
+// 16t..16t+15 and row tile 2t+1 the same rows of up, so 2 ceil(I/16) row tiles in all; a kernel
+// holding an even-aligned pair of row tiles holds matching gate and up rows.
 constexpr int kTileRows = 16;
 constexpr int kTileK = 64;
 constexpr int kTileBytes = 1024;
 
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Four outputs y[m, n..n+cnt) in bf16 (RNE); one aligned 8-byte store when yvec and cnt == 4.
+__device__ __forceinline__ void store_bf16x4(uint16_t* y, int64_t ldy, int m, int n, int cnt,
+                                             const float (&o)[4], bool yvec) {
+  uint16_t* out = y + (int64_t)m * ldy + n;
+  if (cnt == 4 && yvec) {
+    *reinterpret_cast<uint2*>(out) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+  } else {
+    for (int r = 0; r < cnt; ++r) out[r] = f32_to_bf16(o[r]);
+  }
+}
+
+// The scaled fp32 value of accumulator element r: W8A16 v * s, W8A8 (v * sx[m]) * s.
+template <bool I8, typename Acc>
+__device__ __forceinline__ float scaled(Acc v, int r, float sc, float sxm) {
+  if constexpr (I8)
+    return ((float)v[r] * sxm) * sc;
+  else
+    return v[r] * sc;
+}
 
 // The scaled output of one lane's MFMA result: `v` holds rows n..n+3 (cnt of them valid) of
 // token m, `sc` their scales, sxm the token's scale (W8A8). W8A16: y = bf16(v * s[n]); W8A8:
@@ -99,12 +123,7 @@ __device__ __forceinline__ void store_out4(uint16_t* y, int64_t ldy, int32_t* ac
                                            bool yvec) {
   float o[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if constexpr (I8)
-      o[r] = ((float)v[r] * sxm) * sc[r];
-    else
-      o[r] = v[r] * sc[r];
-  }
+  for (int r = 0; r < 4; ++r) o[r] = scaled<I8>(v, r, sc[r], sxm);
   if constexpr (I8) {
     if (acc) {
       int32_t* dst = acc + (int64_t)m * N + n;
@@ -116,12 +135,26 @@ __device__ __forceinline__ void store_out4(uint16_t* y, int64_t ldy, int32_t* ac
     }
     if (!y) return;
   }
-  uint16_t* out = y + (int64_t)m * ldy + n;
-  if (cnt == 4 && yvec) {
-    *reinterpret_cast<uint2*>(out) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
-  } else {
-    for (int r = 0; r < cnt; ++r) out[r] = f32_to_bf16(o[r]);
-  }
+  store_bf16x4(y, ldy, m, n, cnt, o, yvec);
+}
+
+// SiLU(v) = v * sigmoid(v) = v / (1 + e^-v) in fp32. e^-v overflows to +inf for v < -88, where
+// the quotient is the correctly signed zero; the hardware exponential's few-ulp fp32 error is far
+// below the bf16 rounding that follows.
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+// Gate/up epilogue of the fused MLP projection: gate and up accumulators of the same four output
+// columns n..n+3 of token m (cnt valid), their scales sg and su. h = bf16(silu(g) * u) with g and
+// u scaled in fp32 as store_out4 scales them, rounded once.
+template <bool I8, typename Acc>
+__device__ __forceinline__ void store_glu4(uint16_t* y, int64_t ldy, int m, int n, int cnt,
+                                           Acc vg, Acc vu, const float (&sg)[4],
+                                           const float (&su)[4], float sxm, bool yvec) {
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    o[r] = silu(scaled<I8>(vg, r, sg[r], sxm)) * scaled<I8>(vu, r, su[r], sxm);
+  store_bf16x4(y, ldy, m, n, cnt, o, yvec);
 }
 
 // s_waitcnt immediate that waits for all but the `n` most recent vector-memory operations

@@ -21,6 +21,10 @@
 //  * Every summation order depends only on (N, K, the token class of M, the grid), never on M
 //    inside a class or on other rows: results are deterministic and a row's output is the same
 //    inside any batch of its class. No atomics.
+//  * Fused gate/up (GLU): the weight is in the gate/up layout (lse_common.h) and panels hold an
+//    even number of row tiles, so every panel holds matching gate and up rows; the final
+//    reduction adds slice pairs (gate tile, up tile) in one wave, which writes
+//    h = bf16(silu(g) * u) for its I output columns. No K splits.
 //
 // Activations reach the MFMAs from LDS, never by gathering 16 token rows per load from global
 // memory (that pattern runs at a fraction of the cache bandwidth):
@@ -64,6 +68,7 @@ struct SkinnyArgs {
   int units;            // panels * splits
   int NSU;              // super-steps per unit: ceil(ssteps / W) rounded up to a multiple of DW
   void* part;           // S > 1: raw partial sums [S][M][16 nrb], fp32 (W8A16) or int32 (W8A8)
+  int glu;              // gate/up layout: I, the output columns (N = 16 nrb packed rows); else 0
 };
 
 // Register stage of the weight ring: one 1 KB tile per row tile of the panel.
@@ -92,7 +97,7 @@ __host__ __device__ constexpr int skinny_swz_mask(int chunks_per_row) {
   return ((chunks_per_row & -chunks_per_row) < 16 ? (chunks_per_row & -chunks_per_row) : 16) - 1;
 }
 
-template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS>
+template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU>
 __global__ void __launch_bounds__(64 * W)
 skinny_kernel(SkinnyArgs a) {
   using Acc = std::conditional_t<I8, i32x4, f32x4>;
@@ -104,6 +109,7 @@ skinny_kernel(SkinnyArgs a) {
   constexpr int NACC = (!I8 && SLICES == 1) ? 2 : 1;
   static_assert(!XLDS || MT == 1, "activations are staged whole for one token tile only");
   static_assert(DW % DX == 0, "the activation ring index must repeat with the weight ring's");
+  static_assert(!GLU || RT % 2 == 0, "gate/up panels hold whole pairs of row tiles");
   // Streamed activations: a wave's ring slot holds the 16 MT token rows x 64 K-columns of one of
   // its steps, row-major (XROW bytes a row), 16-byte chunks XOR-swizzled by token (chunk c of row
   // m sits at c ^ xstep_swz(m)); the wave fills it with XI pieces of 1 KB.
@@ -118,11 +124,12 @@ skinny_kernel(SkinnyArgs a) {
   constexpr int XWAVE = 16 * MT * XROW / 16;    // uint4 per wave per slot
   constexpr int XSLOT = XLDS ? 1 : W * XWAVE;
   // Slices reduced per pass through LDS: all W waves' partials of RS slices (1 KB each) at once,
-  // as many as the LDS left by the activation ring and the scales holds.
+  // as many as the LDS left by the activation ring and the scales holds (whole gate/up pairs).
   constexpr int kRedBudget = 160 * 1024 - DX * XSLOT * 16 - kSkinnyScaleLds * 4;
   constexpr int RS0 = W < SLICES ? W : SLICES;
-  constexpr int RS = RS0 * W * 1024 <= kRedBudget ? RS0 : kRedBudget / (W * 1024);
-  static_assert(RS >= 1, "no LDS left for the cross-wave reduction");
+  constexpr int RS1 = RS0 * W * 1024 <= kRedBudget ? RS0 : kRedBudget / (W * 1024);
+  constexpr int RS = GLU ? RS1 & ~1 : RS1;
+  static_assert(RS >= (GLU ? 2 : 1), "no LDS left for the cross-wave reduction");
   constexpr int NPASS = (SLICES + RS - 1) / RS;
 
   __shared__ Acc red[W][RS][64];
@@ -163,6 +170,8 @@ skinny_kernel(SkinnyArgs a) {
   // image is bytes [1024 i, 1024 i + 1024), lane l fills byte 1024 i + 16 l, which is physical
   // chunk pc of row m and holds logical chunk pc ^ swz(m); tokens past M and K past the end read
   // zeros, so the image needs no bounds checks when read.
+  // Scales are staged per packed row: in the gate/up layout packed row 16 rb + r is gate
+  // (rb even) or up (rb odd) row 16 (rb / 2) + r, whose scale is s[(rb & 1) I + 16 (rb / 2) + r].
   const int srow0 = 16 * RT * u_first;
   const int nsc = split ? 0 : min(16 * RT * u_end, a.N) - srow0;
   constexpr int kScPerThread = (kSkinnyScaleLds + 64 * W - 1) / (64 * W);
@@ -170,7 +179,14 @@ skinny_kernel(SkinnyArgs a) {
 #pragma unroll
   for (int i = 0; i < kScPerThread; ++i) {
     const int r = threadIdx.x + 64 * W * i;
-    sc_stage[i] = r < nsc ? a.s[srow0 + r] : 0.0f;
+    int src = srow0 + r;
+    bool valid = r < nsc;
+    if constexpr (GLU) {
+      const int rb = src >> 4, o = 16 * (rb >> 1) + (src & 15);
+      valid = valid && o < a.glu;
+      src = (rb & 1) * a.glu + o;
+    }
+    sc_stage[i] = valid ? a.s[src] : 0.0f;
   }
   const int xrow_bytes = skinny_x_row(a.K, ESZ);
   const int xswz = skinny_swz_mask(xrow_bytes / 16);
@@ -336,9 +352,28 @@ skinny_kernel(SkinnyArgs a) {
     for (int r = 0; r < 4; ++r) sc[r] = r < cnt ? s_lds[n + r - srow0] : 0.0f;
     store_out4<I8>(a.y, a.ldy, a.acc, a.N, m, n, cnt, v, sc, sxv[b], yvec);
   };
+  // Gate/up: slice `slice` (an even row tile rt of token tile b) holds gate rows of output
+  // columns 16 (rb / 2) + 4 g + r, slice + 1 the up rows of the same columns.
+  auto store_glu = [&](int p, int slice, Acc vg, Acc vu) {
+    const int rt = slice % RT, b = slice / RT;
+    const int m = 16 * b + r16;
+    const int rb = p * RT + rt;
+    const int n = 16 * (rb >> 1) + 4 * g;
+    if (m >= a.M || n >= a.glu) return;
+    const int cnt = min(4, a.glu - n);
+    const int pr = 16 * rb + 4 * g - srow0;  // packed row of the first gate output
+    float sg[4], su[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sg[r] = r < cnt ? s_lds[pr + r] : 0.0f;
+      su[r] = r < cnt ? s_lds[pr + 16 + r] : 0.0f;
+    }
+    store_glu4<I8>(a.y, a.ldy, m, n, cnt, vg, vu, sg, su, sxv[b], yvec);
+  };
 
   // End of a unit (panel p of split sp): pass i adds slices [i RS, i RS + RS) over the waves in
-  // wave order; wave w < RS keeps slice i RS + w and stores it.
+  // wave order; wave w < RS keeps slice i RS + w and stores it (gate/up: wave w < RS / 2 keeps
+  // the pair i RS + 2 w, i RS + 2 w + 1).
   auto unit_end = [&](int p, int sp) {
 #pragma unroll
     for (int i = 0; i < NPASS; ++i) {
@@ -354,12 +389,25 @@ skinny_kernel(SkinnyArgs a) {
           red[wave][sl][lane] = v;
         }
       __syncthreads();
-      const int slice = wave + RS * i;
-      if (wave < RS && slice < SLICES) {
-        Acc v = red[0][wave][lane];
+      if constexpr (GLU) {
+        const int slice = 2 * wave + RS * i;
+        if (2 * wave < RS && slice < SLICES) {
+          Acc vg = red[0][2 * wave][lane], vu = red[0][2 * wave + 1][lane];
 #pragma unroll
-        for (int w2 = 1; w2 < W; ++w2) v += red[w2][wave][lane];
-        store_out(p, sp, slice, v);
+          for (int w2 = 1; w2 < W; ++w2) {
+            vg += red[w2][2 * wave][lane];
+            vu += red[w2][2 * wave + 1][lane];
+          }
+          store_glu(p, slice, vg, vu);
+        }
+      } else {
+        const int slice = wave + RS * i;
+        if (wave < RS && slice < SLICES) {
+          Acc v = red[0][wave][lane];
+#pragma unroll
+          for (int w2 = 1; w2 < W; ++w2) v += red[w2][wave][lane];
+          store_out(p, sp, slice, v);
+        }
       }
     }
 #pragma unroll
@@ -437,9 +485,9 @@ struct SkinnyShape {
   int splits;
 };
 
-template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS>
+template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU = false>
 static const void* skinny_fn() {
-  return reinterpret_cast<const void*>(&skinny_kernel<I8, MT, RT, W, DW, DX, XLDS>);
+  return reinterpret_cast<const void*>(&skinny_kernel<I8, MT, RT, W, DW, DX, XLDS, GLU>);
 }
 
 // Panel height for 17..64 tokens: each panel re-reads the activations from L2, so panels are as
@@ -458,35 +506,42 @@ static bool skinny_split_k(int64_t N, int64_t K) {
   return ceil_div(N, kTileRows) <= 256 && ceil_div(K, kTileK) >= 128;
 }
 
+// N counts packed rows (2 x 16 ceil(I / 16) in the gate/up layout, whose panels hold at least
+// one pair of row tiles and are never split over K).
 template <bool I8>
-static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K) {
+static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K, bool glu = false) {
   if (M <= 16) {
     const bool fits = M * (size_t)skinny_x_row((int)K, I8 ? 1 : 2) <= (size_t)kSkinnyXLdsBytes;
-    return {1, 1, 8, 4, fits, 1};
+    return {1, glu ? 2 : 1, 8, 4, fits, 1};
   }
   const int mt = M <= 32 ? 2 : 4;
-  if (skinny_split_k(N, K)) return {mt, 4, 4, 4, false, 4};
-  const int rt = skinny_rt(N);
+  if (!glu && skinny_split_k(N, K)) return {mt, 4, 4, 4, false, 4};
+  const int rt = std::max(skinny_rt(N), glu ? 2 : 1);
   if (mt == 2) return {2, rt, rt == 4 ? 4 : 8, 4, false, 1};
   // 64 tokens: two waves per SIMD (eight per workgroup, shallower rings) for 32- and 64-row
   // panels, one per SIMD with a deeper ring for single row tiles.
   return rt == 1 ? SkinnyShape{4, 1, 4, 4, false, 1} : SkinnyShape{4, rt, 8, 2, false, 1};
 }
 
-template <bool I8>
+template <bool I8, bool GLU = false>
 static const void* skinny_kernel_for(const SkinnyShape& sh) {
-  if (sh.mt == 1) {
-    return sh.xlds ? skinny_fn<I8, 1, 1, 8, 4, 1, true>() : skinny_fn<I8, 1, 1, 8, 4, 4, false>();
+  if constexpr (GLU) {
+    if (sh.mt == 1)
+      return sh.xlds ? skinny_fn<I8, 1, 2, 8, 4, 1, true, true>()
+                     : skinny_fn<I8, 1, 2, 8, 4, 4, false, true>();
+  } else {
+    if (sh.mt == 1)
+      return sh.xlds ? skinny_fn<I8, 1, 1, 8, 4, 1, true>() : skinny_fn<I8, 1, 1, 8, 4, 4, false>();
+    if (sh.rt == 1)
+      return sh.mt == 2 ? skinny_fn<I8, 2, 1, 8, 4, 4, false>() : skinny_fn<I8, 4, 1, 4, 4, 4, false>();
+    if (sh.mt == 4 && sh.rt == 4 && sh.w == 4) return skinny_fn<I8, 4, 4, 4, 4, 2, false>();
   }
   if (sh.mt == 2) {
-    if (sh.rt == 1) return skinny_fn<I8, 2, 1, 8, 4, 4, false>();
-    if (sh.rt == 2) return skinny_fn<I8, 2, 2, 8, 4, 2, false>();
-    return skinny_fn<I8, 2, 4, 4, 4, 4, false>();
+    if (sh.rt == 2) return skinny_fn<I8, 2, 2, 8, 4, 2, false, GLU>();
+    return skinny_fn<I8, 2, 4, 4, 4, 4, false, GLU>();
   }
-  if (sh.rt == 1) return skinny_fn<I8, 4, 1, 4, 4, 4, false>();
-  if (sh.rt == 2) return skinny_fn<I8, 4, 2, 8, 2, 2, false>();
-  if (sh.w == 8) return skinny_fn<I8, 4, 4, 8, 2, 2, false>();
-  return skinny_fn<I8, 4, 4, 4, 4, 2, false>();
+  if (sh.rt == 2) return skinny_fn<I8, 4, 2, 8, 2, 2, false, GLU>();
+  return skinny_fn<I8, 4, 4, 8, 2, 2, false, GLU>();
 }
 
 struct SkinnyPlan {
@@ -531,10 +586,15 @@ static SkinnyPlan skinny_plan_for(const SkinnyShape& sh, const void* fn, int64_t
   return pl;
 }
 
+// glu > 0: the gate/up layout of two (glu, K) matrices (N is then ignored).
 template <bool I8>
-static SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
-  const SkinnyShape sh = skinny_shape<I8>(M, N, K);
-  return skinny_plan_for<I8>(sh, skinny_kernel_for<I8>(sh), M, N, K);
+static SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t glu = 0) {
+  if (glu > 0) N = 2 * kTileRows * ceil_div(glu, kTileRows);
+  const SkinnyShape sh = skinny_shape<I8>(M, N, K, glu > 0);
+  SkinnyPlan pl = skinny_plan_for<I8>(
+      sh, glu > 0 ? skinny_kernel_for<I8, true>(sh) : skinny_kernel_for<I8>(sh), M, N, K);
+  pl.a.glu = (int)glu;
+  return pl;
 }
 
 // Launches a planned call: the unit kernel, then (S > 1) the reduction over the splits. The
@@ -558,36 +618,49 @@ int64_t skinny_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K) {
   return i8 ? skinny_plan<true>(M, N, K).part_bytes : skinny_plan<false>(M, N, K).part_bytes;
 }
 
-int launch_w8a16_skinny(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
-                        uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
-                        int64_t ws_bytes, hipStream_t stream) {
-  SkinnyPlan pl = skinny_plan<false>(M, N, K);
+template <bool I8>
+static int skinny_run(const void* x, int64_t ldx, const int8_t* qp, const float* s,
+                      const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
+                      int64_t N, int64_t K, int64_t glu, void* ws, int64_t ws_bytes,
+                      hipStream_t stream) {
+  SkinnyPlan pl = skinny_plan<I8>(M, N, K, glu);
   if (ws_bytes < pl.part_bytes || (pl.part_bytes && !ws)) return LSE_E_WORKSPACE;
   SkinnyArgs& a = pl.a;
   a.x = x;
   a.ldx = ldx;
   a.qp = qp;
   a.s = s;
+  a.sx = sx;
   a.y = y;
   a.ldy = ldy;
-  return skinny_launch<false>(pl, ws, stream);
+  a.acc = acc;
+  return skinny_launch<I8>(pl, ws, stream);
+}
+
+int launch_w8a16_skinny(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                        uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                        int64_t ws_bytes, hipStream_t stream) {
+  return skinny_run<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, 0, ws, ws_bytes,
+                           stream);
 }
 
 int launch_w8a8_skinny(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
                        uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
                        void* ws, int64_t ws_bytes, hipStream_t stream) {
-  SkinnyPlan pl = skinny_plan<true>(M, N, K);
-  if (ws_bytes < pl.part_bytes || (pl.part_bytes && !ws)) return LSE_E_WORKSPACE;
-  SkinnyArgs& a = pl.a;
-  a.x = xq;
-  a.ldx = K;
-  a.qp = qp;
-  a.s = s;
-  a.sx = sx;
-  a.y = y;
-  a.ldy = ldy;
-  a.acc = acc;
-  return skinny_launch<true>(pl, ws, stream);
+  return skinny_run<true>(xq, K, qp, s, sx, y, ldy, acc, M, N, K, 0, ws, ws_bytes, stream);
+}
+
+int launch_w8a16_skinny_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                            uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                            hipStream_t stream) {
+  return skinny_run<false>(x, ldx, qp, s, nullptr, h, ldh, nullptr, M, 0, K, I, nullptr, 0,
+                           stream);
+}
+
+int launch_w8a8_skinny_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                           uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                           hipStream_t stream) {
+  return skinny_run<true>(xq, K, qp, s, sx, h, ldh, nullptr, M, 0, K, I, nullptr, 0, stream);
 }
 
 }  // namespace lse

@@ -32,6 +32,11 @@
 //
 // Summation order: the K steps in increasing order, two K=32 MFMAs per step (W8A16) in a fixed
 // chain per output; it depends only on K. int32 accumulation (W8A8) is exact in any order.
+//
+// Fused gate/up (GLU): with the weight in the gate/up layout (lse_common.h) a block's first row
+// tile is even and a wave's TN row tiles are an even-aligned run, so its tiles j (even, gate) and
+// j + 1 (up) hold the same output columns in the same lanes; the epilogue writes
+// h = bf16(silu(g) * u) for them.
 #include <algorithm>
 #include <type_traits>
 
@@ -52,6 +57,7 @@ struct TiledArgs {
   int nsteps;        // ceil(K / 64)
   int nrb;           // ceil(N / 16)
   int mblocks, nblocks;
+  int glu;           // gate/up layout: I, the output columns (N = 16 nrb packed rows); else 0
 };
 
 constexpr int kGroupM = 4;
@@ -65,7 +71,7 @@ __device__ __forceinline__ int tiled_swz(int r) {
   return I8 ? (r >> 2) & 3 : (r >> 1) & 7;
 }
 
-template <bool I8, int BM, int BN, int WGM, int WGN, int NST>
+template <bool I8, int BM, int BN, int WGM, int WGN, int NST, bool GLU>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 tiled_gemm_kernel(TiledArgs a) {
   using Acc = std::conditional_t<I8, i32x4, f32x4>;
@@ -84,6 +90,7 @@ tiled_gemm_kernel(TiledArgs a) {
   static_assert(XBYTES % (W * 1024) == 0 && WTILES % W == 0, "whole 1 KB loads per wave");
   static_assert(NST >= 3 && NST <= 4, "three or four stage slots");
   static_assert((NST - 2) * LOADS < 64, "vmcnt holds at most 63");
+  static_assert(!GLU || TN % 2 == 0, "gate/up wave tiles hold whole pairs of row tiles");
 
   // One LDS array per stage slot (x image, then the weight tiles).
   constexpr int SLOT = (XBYTES + WTILES * 1024) / 16;
@@ -220,6 +227,29 @@ tiled_gemm_kernel(TiledArgs a) {
 
   // Epilogue. D tile (i, j): lane holds weight rows 4 g + r (r = 0..3) of token r16.
   const bool yvec = a.y && (a.ldy & 3) == 0 && ((uintptr_t)a.y & 7) == 0;
+  if constexpr (GLU) {
+    // Row tile rb = rb0 + wn TN + j (even j: gate) covers output columns 16 (rb / 2) + 4 g + r.
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * WM + 16 * i + r16;
+      if (m >= a.M) continue;
+      const float sxm = I8 ? a.sx[m] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < TN; j += 2) {
+        const int n = 16 * ((rb0 + wn * TN + j) >> 1) + 4 * g;
+        if (n >= a.glu) continue;
+        const int cnt = min(4, a.glu - n);
+        float sg[4], su[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sg[r] = r < cnt ? a.s[n + r] : 0.0f;
+          su[r] = r < cnt ? a.s[a.glu + n + r] : 0.0f;
+        }
+        store_glu4<I8>(a.y, a.ldy, m, n, cnt, acc[i][j], acc[i][j + 1], sg, su, sxm, yvec);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int m = m0 + wm * WM + 16 * i + r16;
@@ -244,21 +274,21 @@ struct TiledShape {
   int bm, bn;
 };
 
-template <bool I8, int BM, int BN>
+template <bool I8, int BM, int BN, bool GLU>
 static const void* tiled_fn() {
   // LDS per block: NST x (x stage + weight stage) <= 160 KB; 128 x 128 tiles keep two blocks
   // per CU.
   constexpr int nst = I8 ? 4 : 3;
   return reinterpret_cast<const void*>(
-      &tiled_gemm_kernel<I8, BM, BN, kTiledWgm, kTiledWgn, nst>);
+      &tiled_gemm_kernel<I8, BM, BN, kTiledWgm, kTiledWgn, nst, GLU>);
 }
 
-template <bool I8>
+template <bool I8, bool GLU>
 static const void* tiled_kernel_for(const TiledShape& sh) {
-  if (sh.bm == 256 && sh.bn == 256) return tiled_fn<I8, 256, 256>();
-  if (sh.bm == 256 && sh.bn == 128) return tiled_fn<I8, 256, 128>();
-  if (sh.bm == 128 && sh.bn == 256) return tiled_fn<I8, 128, 256>();
-  return tiled_fn<I8, 128, 128>();
+  if (sh.bm == 256 && sh.bn == 256) return tiled_fn<I8, 256, 256, GLU>();
+  if (sh.bm == 256 && sh.bn == 128) return tiled_fn<I8, 256, 128, GLU>();
+  if (sh.bm == 128 && sh.bn == 256) return tiled_fn<I8, 128, 256, GLU>();
+  return tiled_fn<I8, 128, 128, GLU>();
 }
 
 // The tile that minimizes (rounds of resident blocks) x (CU time per round) = rounds x tile area
@@ -294,10 +324,12 @@ static int device_cus() {
   return cus;
 }
 
+// glu > 0: the gate/up layout of two (glu, K) matrices, N = 2 x 16 ceil(glu / 16) packed rows.
 template <bool I8>
 static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const float* s,
                         const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
-                        int64_t N, int64_t K, hipStream_t stream) {
+                        int64_t N, int64_t K, int64_t glu, hipStream_t stream) {
+  if (glu > 0) N = 2 * kTileRows * ceil_div(glu, kTileRows);
   const TiledShape sh = tiled_shape(M, N, device_cus());
   TiledArgs a{};
   a.x = x;
@@ -315,24 +347,38 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
   a.nrb = (int)ceil_div(N, kTileRows);
   a.mblocks = (int)ceil_div(M, sh.bm);
   a.nblocks = (int)ceil_div(N, sh.bn);
+  a.glu = (int)glu;
   const int64_t blocks = (int64_t)a.mblocks * a.nblocks;
   if (blocks > 0x7fffffff) return LSE_E_RANGE;
   void* args[] = {&a};
-  const hipError_t e = hipLaunchKernel(tiled_kernel_for<I8>(sh), dim3((unsigned)blocks),
-                                       dim3(kTiledThreads), args, 0, stream);
+  const void* fn = glu > 0 ? tiled_kernel_for<I8, true>(sh) : tiled_kernel_for<I8, false>(sh);
+  const hipError_t e =
+      hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(kTiledThreads), args, 0, stream);
   return e == hipSuccess ? launch_status() : (int)e;
 }
 
 int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
                       uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                       hipStream_t stream) {
-  return launch_tiled<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, stream);
+  return launch_tiled<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, 0, stream);
 }
 
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
                      uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
                      hipStream_t stream) {
-  return launch_tiled<true>(xq, K, qp, s, sx, y, ldy, acc, M, N, K, stream);
+  return launch_tiled<true>(xq, K, qp, s, sx, y, ldy, acc, M, N, K, 0, stream);
+}
+
+int launch_w8a16_gemm_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                          uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                          hipStream_t stream) {
+  return launch_tiled<false>(x, ldx, qp, s, nullptr, h, ldh, nullptr, M, 0, K, I, stream);
+}
+
+int launch_w8a8_gemm_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                         uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                         hipStream_t stream) {
+  return launch_tiled<true>(xq, K, qp, s, sx, h, ldh, nullptr, M, 0, K, I, stream);
 }
 
 }  // namespace lse

@@ -13,12 +13,15 @@ applies o_proj (`attention_output`, model_runner.py:365-369).
 `DecodeRunner` runs exactly that sequence over HF Llama modules, with two linear back ends:
   * "bf16": the reference's own `nn.Linear` modules (q, k, v, o, gate, up, down: seven GEMMs a
     layer on the vendor BLAS);
-  * "int8" / "w8a8": `Int8Linear` on the fused shapes the kernels are tuned for (one (4096, 6144)
-    QKV projection and one (4096, 28672) gate_up projection, split after the GEMM), o_proj and
-    down_proj. Per-channel quantization of a row-stacked weight equals quantizing each part;
+  * "int8" / "w8a8": `Int8Linear` on the fused (4096, 6144) QKV shape the kernels are tuned for
+    (split after the GEMM), o_proj and down_proj, and `Int8GateUp` for gate/up: one (4096, 28672)
+    weight stream whose epilogue applies the MLP's SiLU-mul, so the (M, 28672) projection never
+    leaves the kernel. Per-channel quantization of a row-stacked weight equals quantizing each
+    part;
   * "int8-torch": the same quantized weights, applied by an eager torch restatement of W8A16
-    (x and q·s in fp32, one fp32 matmul, bf16 out) instead of the HIP kernels; it isolates the
-    kernels from the quantization itself. Test and measurement use only.
+    (x and q·s in fp32, one fp32 matmul, bf16 out; gate/up as bf16 projections, then SiLU-mul,
+    as the reference's LlamaMLP rounds them) instead of the HIP kernels; it isolates the kernels
+    from the quantization itself. Test and measurement use only.
 lm_head stays bf16 in both. Attention runs in fp32 over a contiguous per-layer KV cache (the
 reference's `contiguous_attention` path, model_runner.py:400-418), so both back ends see the
 same attention arithmetic and only the linears differ.
@@ -31,7 +34,7 @@ import math
 import torch
 from torch import nn
 
-from .int8_linear import Int8Linear
+from .int8_linear import Int8GateUp, Int8Linear
 
 LLAMA3_8B = dict(
     hidden_size=4096,
@@ -89,14 +92,13 @@ class DecodeRunner:
         for layer in self.layers:
             attn, mlp = layer.self_attn, layer.mlp
             qkv = torch.cat([attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight])
-            gate_up = torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight])
             self.int8.append({
                 "qkv": _int8(qkv, mode),
                 "o": _int8(attn.o_proj.weight, mode),
-                "gate_up": _int8(gate_up, mode),
+                "gate_up": Int8GateUp.from_linears(mlp.gate_proj, mlp.up_proj, mode),
                 "down": _int8(mlp.down_proj.weight, mode),
             })
-            del qkv, gate_up
+            del qkv
         torch.cuda.empty_cache()
 
     def use(self, backend: str) -> None:
@@ -130,6 +132,8 @@ class DecodeRunner:
         mlp = self.layers[i].mlp
         if self.backend == "bf16":
             return mlp(x)
+        if self.backend == "int8":
+            return self._lin(i, "down", self.int8[i]["gate_up"](x))
         gu = self._lin(i, "gate_up", x)
         inter = gu.shape[-1] // 2
         return self._lin(i, "down", mlp.act_fn(gu[..., :inter]) * gu[..., inter:])
@@ -224,10 +228,15 @@ class DecodeRunner:
         out), excluding lm_head."""
         total = 0
         for mod, x in self.linear_calls(m):
-            k, n = x.shape[-1], mod.out_features
-            if isinstance(mod, Int8Linear):
+            k = x.shape[-1]
+            if isinstance(mod, Int8GateUp):  # both weights in, the SiLU-mul product out
+                n = 2 * mod.intermediate_size
+                total += k * n + 4 * n + 2 * m * k + 2 * m * (n // 2)
+            elif isinstance(mod, Int8Linear):
+                n = mod.out_features
                 total += k * n + 4 * n + 2 * m * k + 2 * m * n
             else:
+                n = mod.out_features
                 total += 2 * k * n + 2 * m * k + 2 * m * n
         return total
 

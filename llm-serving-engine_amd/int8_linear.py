@@ -9,6 +9,11 @@ buffers, not Parameters: the runner reads `model.dtype` off the first parameter
 
 `qweight` holds the int8 weight in the packed tile layout the kernels stream (ops.pack_weight),
 shape (ceil(N/16), ceil(K/64), 1024); `unpacked_qweight()` returns the row-major (N, K) matrix.
+
+`Int8GluMLP` is the drop-in for the whole `LlamaMLP` (transformers modeling_llama.py:163-176),
+which the runner calls as `layer.mlp(x)` (model_runner.py:223): its gate and up projections and
+the SiLU-mul between them (`down_proj(act_fn(gate_proj(x)) * up_proj(x))`, line 175) run as one
+`Int8GateUp` kernel, then `down_proj` as an `Int8Linear`.
 """
 
 from __future__ import annotations
@@ -110,3 +115,104 @@ def check_linear_supported(linear: nn.Linear) -> None:
     max_k = _lib.query(_lib.Q_MAX_K)
     if linear.in_features > max_k:
         raise RuntimeError(f"int8 kernels take in_features <= {max_k}, got {linear.in_features}")
+
+
+def _is_silu(act: nn.Module) -> bool:
+    # transformers' ACT2FN["silu"] is its own SiLUActivation (activations.py), calling F.silu.
+    return isinstance(act, nn.SiLU) or type(act).__name__ == "SiLUActivation"
+
+
+class Int8GateUp(nn.Module):
+    """h = silu(x · (q_g · diag(s_g))ᵀ) * (x · (q_u · diag(s_u))ᵀ), x (..., K) → h (..., I) bf16:
+    the gate and up projections of `LlamaMLP` and its SiLU-mul (modeling_llama.py:175) as one
+    int8 GEMM whose epilogue applies the activation and the product in fp32 and rounds once.
+
+    `qweight` holds the stacked (2I, K) [gate; up] weight in the gate/up layout (ops.pack_glu),
+    `scales` the (2I,) [gate; up] per-channel scales."""
+
+    def __init__(
+        self,
+        in_features: int,
+        intermediate_size: int,
+        mode: str = "int8",
+        device: torch.device | str | None = None,
+    ) -> None:
+        super().__init__()
+        if mode not in MODES:
+            raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
+        self.in_features = in_features
+        self.intermediate_size = intermediate_size
+        self.mode = mode
+        self.register_buffer(
+            "qweight",
+            torch.zeros(ops.packed_glu_shape(intermediate_size, in_features), dtype=torch.int8,
+                        device=device),
+        )
+        self.register_buffer(
+            "scales", torch.ones((2 * intermediate_size,), dtype=torch.float32, device=device))
+
+    @classmethod
+    def from_linears(cls, gate: nn.Linear, up: nn.Linear, mode: str = "int8") -> Int8GateUp:
+        """Quantizes the bias-free `gate` and `up` projections per output channel."""
+        for lin in (gate, up):
+            check_linear_supported(lin)
+            if lin.bias is not None:
+                raise RuntimeError("the fused gate/up kernel takes bias-free projections")
+        if gate.weight.shape != up.weight.shape:
+            raise RuntimeError(
+                f"gate and up shapes differ: {tuple(gate.weight.shape)} vs {tuple(up.weight.shape)}")
+        q_g, s_g = ops.quantize_weight_per_channel(gate.weight.detach())
+        q_u, s_u = ops.quantize_weight_per_channel(up.weight.detach())
+        return cls.from_quantized(torch.cat([q_g, q_u]), torch.cat([s_g, s_u]), mode)
+
+    @classmethod
+    def from_quantized(cls, qweight: torch.Tensor, scales: torch.Tensor,
+                       mode: str = "int8") -> Int8GateUp:
+        """Wraps an already quantized stacked (2I, K) int8 [gate; up] weight and its (2I,) fp32
+        scales (on the GPU; packed there)."""
+        two_i, k = qweight.shape
+        mod = cls(k, two_i // 2, mode, qweight.device)
+        mod.qweight.copy_(ops.pack_glu(qweight))
+        mod.scales.copy_(scales)
+        return mod
+
+    def unpacked_qweight(self) -> torch.Tensor:
+        """The stacked (2I, K) int8 [gate; up] weight, row-major."""
+        return ops.unpack_glu(self.qweight, self.intermediate_size, self.in_features)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.mode == "int8":
+            return ops.w8a16_glu(x, self.qweight, self.scales)
+        return ops.w8a8_glu(x, self.qweight, self.scales)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, intermediate_size={self.intermediate_size}, "
+                f"mode={self.mode}")
+
+
+class Int8GluMLP(nn.Module):
+    """Drop-in for `LlamaMLP` (modeling_llama.py:163-176): forward(x) = down_proj(gate_up(x))."""
+
+    def __init__(self, gate_up: Int8GateUp, down_proj: Int8Linear) -> None:
+        super().__init__()
+        self.gate_up = gate_up
+        self.down_proj = down_proj
+
+    @classmethod
+    def from_mlp(cls, mlp: nn.Module, mode: str = "int8") -> Int8GluMLP:
+        """Quantizes a `LlamaMLP` (gate_proj, up_proj, down_proj, SiLU act_fn, no bias)."""
+        if not _is_silu(mlp.act_fn):
+            raise RuntimeError(
+                f"the fused gate/up kernel applies SiLU, the MLP uses {type(mlp.act_fn).__name__}")
+        return cls(Int8GateUp.from_linears(mlp.gate_proj, mlp.up_proj, mode),
+                   Int8Linear.from_linear(mlp.down_proj, mode))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(self.gate_up(x))
+
+
+def fusable_mlp(mlp: nn.Module) -> bool:
+    """Whether `mlp` has the LlamaMLP form the fused gate/up kernel computes."""
+    parts = [getattr(mlp, n, None) for n in ("gate_proj", "up_proj", "down_proj")]
+    return (all(isinstance(p, nn.Linear) for p in parts) and _is_silu(getattr(mlp, "act_fn", None))
+            and parts[0].bias is None and parts[1].bias is None)

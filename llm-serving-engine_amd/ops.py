@@ -5,7 +5,9 @@ into a graph.
 
 Weights are held in the packed tile layout the kernels stream (`pack_weight`): a (N, K) int8
 matrix becomes a (ceil(N/16), ceil(K/64), 1024) int8 tensor whose 1 KB tiles are 16 rows x 64
-K-bytes each, in matrix-core operand order.
+K-bytes each, in matrix-core operand order. The MLP's gate and up weights share one tensor in the
+gate/up layout (`pack_glu`): row tile 2t holds gate rows 16t..16t+15, row tile 2t+1 the same up
+rows, so one kernel computes both and applies SiLU-mul before anything leaves registers.
 """
 
 from __future__ import annotations
@@ -15,13 +17,18 @@ import torch
 from . import _lib
 
 __all__ = [
+    "pack_glu",
     "pack_weight",
+    "packed_glu_shape",
     "packed_shape",
     "quantize_act_per_token",
     "quantize_weight_per_channel",
+    "unpack_glu",
     "unpack_weight",
     "w8a8_gemm",
+    "w8a8_glu",
     "w8a8_linear",
+    "w8a16_glu",
     "w8a16_linear",
     "workspace",
 ]
@@ -81,6 +88,33 @@ def unpack_weight(qp: torch.Tensor, n: int, k: int) -> torch.Tensor:
     return t[:n, :k].contiguous()
 
 
+def packed_glu_shape(i: int, k: int) -> tuple[int, int, int]:
+    return (2 * ((i + 15) // 16), (k + 63) // 64, 1024)
+
+
+def pack_glu(q: torch.Tensor) -> torch.Tensor:
+    """Stacked row-major (2I, K) int8 [gate; up] → the gate/up layout, (2 ceil(I/16), ceil(K/64),
+    1024) int8, on the GPU."""
+    _require(q.dim() == 2 and q.dtype == torch.int8 and q.shape[0] % 2 == 0,
+             "q must be a 2-D int8 tensor of 2I stacked gate and up rows")
+    dev = _on_gpu(q)
+    i, k = q.shape[0] // 2, q.shape[1]
+    q = q.contiguous()
+    qp = torch.empty(packed_glu_shape(i, k), dtype=torch.int8, device=dev)
+    _lib.check(_lib.library().lse_pack_glu(q.data_ptr(), i, k, qp.data_ptr(), _stream(dev)),
+               "lse_pack_glu")
+    return qp
+
+
+def unpack_glu(qp: torch.Tensor, i: int, k: int) -> torch.Tensor:
+    """Inverse of `pack_glu`: the stacked (2I, K) int8 [gate; up]."""
+    rows = unpack_weight(qp, qp.shape[0] * 16, k)  # packed rows, tile pairs (gate, up)
+    pairs = rows.reshape(-1, 2, 16, k)
+    gate = pairs[:, 0].reshape(-1, k)[:i]
+    up = pairs[:, 1].reshape(-1, k)[:i]
+    return torch.cat([gate, up]).contiguous()
+
+
 def workspace(mode: int, m: int, n: int, k: int, dev: torch.device) -> torch.Tensor | None:
     """The workspace one decode-kernel call needs (some shapes add partial sums of K ranges in a
     second pass), or None. Allocated with torch.empty, so graph-pool owned under capture; the
@@ -94,11 +128,18 @@ def _ws_args(ws: torch.Tensor | None) -> tuple[int | None, int]:
     return (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
 
 
-def _check_packed(qp: torch.Tensor, n: int, k: int) -> None:
+def _check_packed(qp: torch.Tensor, n: int, k: int, glu: bool = False) -> None:
     _require(qp.dtype == torch.int8 and qp.is_contiguous(), "packed weight must be contiguous int8")
-    _require(tuple(qp.shape) == packed_shape(n, k),
-             f"packed weight has shape {tuple(qp.shape)}, (N, K) = ({n}, {k}) needs "
-             f"{packed_shape(n, k)}")
+    want = packed_glu_shape(n, k) if glu else packed_shape(n, k)
+    what = "(I, K)" if glu else "(N, K)"
+    _require(tuple(qp.shape) == want,
+             f"packed weight has shape {tuple(qp.shape)}, {what} = ({n}, {k}) needs {want}")
+
+
+def _glu_scales(scales: torch.Tensor) -> int:
+    _require(scales.dtype == torch.float32 and scales.dim() == 1 and scales.shape[0] % 2 == 0,
+             "gate/up scales must be fp32 (2I,) [gate; up]")
+    return scales.shape[0] // 2
 
 
 # ---- ops -------------------------------------------------------------------------------------
@@ -211,3 +252,49 @@ def w8a8_linear(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor) -> torc
     xq, sx = quantize_act_per_token(x)
     y, _ = w8a8_gemm(xq, sx, qp, scales)
     return y.view(*x.shape[:-1], n)
+
+
+def w8a16_glu(
+    x: torch.Tensor,
+    qp: torch.Tensor,
+    scales: torch.Tensor,
+    algo: int = _lib.ALGO_AUTO,
+) -> torch.Tensor:
+    """h = bf16(silu(g) * u) for x (..., K) bf16 → h (..., I) bf16, where g and u are the fp32
+    W8A16 products of x with the gate and up weights (`pack_glu` layout, scales (2I,) [gate;
+    up]); one kernel, one rounding."""
+    dev = _on_gpu(x, qp, scales)
+    _require(x.dtype == torch.bfloat16, f"W8A16 expects bf16 activations, got {x.dtype}")
+    i, k = _glu_scales(scales), x.shape[-1]
+    _check_packed(qp, i, k, glu=True)
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    h = torch.empty((m, i), dtype=torch.bfloat16, device=dev)
+    ldx = x2.stride(0) if m > 1 else k
+    _lib.check(
+        _lib.library().lse_w8a16_glu(
+            x2.data_ptr(), ldx, qp.data_ptr(), scales.data_ptr(), h.data_ptr(), i, m, i, k, algo,
+            _stream(dev),
+        ),
+        "lse_w8a16_glu",
+    )
+    return h.view(*x.shape[:-1], i)
+
+
+def w8a8_glu(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """Dynamic per-token W8A8 form of `w8a16_glu`: x quantized per row, exact int32 sums,
+    g = (acc_g * sx) * s_g, u likewise, h = bf16(silu(g) * u). x (..., K) → h (..., I)."""
+    dev = _on_gpu(x, qp, scales)
+    i = _glu_scales(scales)
+    xq, sx = quantize_act_per_token(x)
+    m, k = xq.shape
+    _check_packed(qp, i, k, glu=True)
+    h = torch.empty((m, i), dtype=torch.bfloat16, device=dev)
+    _lib.check(
+        _lib.library().lse_w8a8_glu(
+            xq.data_ptr(), sx.data_ptr(), qp.data_ptr(), scales.data_ptr(), h.data_ptr(), i, m, i,
+            k, _stream(dev),
+        ),
+        "lse_w8a8_glu",
+    )
+    return h.view(*x.shape[:-1], i)

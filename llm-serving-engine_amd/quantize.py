@@ -16,7 +16,7 @@ import gc
 import torch
 from torch import nn
 
-from .int8_linear import MODES, Int8Linear
+from .int8_linear import MODES, Int8GluMLP, Int8Linear, fusable_mlp
 
 ATTENTION_PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj")
 MLP_PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
@@ -38,14 +38,21 @@ def check_int8_support(model: nn.Module) -> None:
 
 
 @torch.no_grad()
-def quantize_model_(model: nn.Module, mode: str = "int8") -> nn.Module:
-    """Replaces q/k/v/o and gate/up/down of every decoder layer by `Int8Linear` (per-channel
-    int8 weights quantized on the GPU). Returns the same model object."""
+def quantize_model_(model: nn.Module, mode: str = "int8", fuse_mlp: bool = True) -> nn.Module:
+    """Replaces q/k/v/o of every decoder layer by `Int8Linear` (per-channel int8 weights
+    quantized on the GPU) and its MLP by `Int8GluMLP` (fused gate/up + SiLU-mul, then down), or,
+    with `fuse_mlp=False` or an MLP of another form, gate/up/down by `Int8Linear` each. Returns
+    the same model object."""
     if mode not in MODES:
         raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
     check_int8_support(model)
     for layer in model.model.layers:
-        for parent, names in ((layer.self_attn, ATTENTION_PROJECTIONS), (layer.mlp, MLP_PROJECTIONS)):
+        swaps = [(layer.self_attn, ATTENTION_PROJECTIONS)]
+        if fuse_mlp and fusable_mlp(layer.mlp):
+            layer.mlp = Int8GluMLP.from_mlp(layer.mlp, mode)
+        else:
+            swaps.append((layer.mlp, MLP_PROJECTIONS))
+        for parent, names in swaps:
             for name in names:
                 linear = getattr(parent, name)
                 if isinstance(linear, nn.Linear):

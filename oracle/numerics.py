@@ -16,7 +16,10 @@ define it:
 * per-output-channel weights: s[n] = max_k |W[n,k]| / 127, q = clamp(rne(W / s), -127, 127);
 * W8A16: y[m,n] = bf16(s[n] * sum_k x[m,k] * q[n,k]), fp32 accumulation;
 * W8A8: sx[m] = max_k |x[m,k]| / 127, xq = clamp(rne(x / sx), -127, 127),
-  acc = sum_k xq * q exactly in int32, y = bf16((fp32(acc) * sx[m]) * s[n]).
+  acc = sum_k xq * q exactly in int32, y = bf16((fp32(acc) * sx[m]) * s[n]);
+* fused gate/up (the MLP's `act_fn(gate_proj(x)) * up_proj(x)`, transformers
+  modeling_llama.py:175, act_fn = SiLU): h = silu(g) * u with g, u the two projections above,
+  silu(v) = v * sigmoid(v) (torch.nn.functional.silu, which transformers' SiLUActivation calls).
 
 All-zero rows are not defined by the specification; this oracle fixes s = 1, q = 0.
 
@@ -160,3 +163,60 @@ def seeded_inputs(
         cols = rng.permutation(k)[: int(round(0.001 * k))]
         x[:, cols] *= np.float32(20.0)
     return f32_to_bf16_bits(x), w
+
+
+# ---- fused gate/up (LlamaMLP's SiLU-mul) ---------------------------------------------------
+
+
+def pack_glu(q: np.ndarray) -> np.ndarray:
+    """Stacked row-major (2I, K) int8 [gate; up] → the gate/up packed layout,
+    (2 ceil(I/16), ceil(K/64), 1024): row tile 2t is pack_weight(gate)'s tile t, row tile 2t+1
+    pack_weight(up)'s tile t (zero past I). A storage permutation of this build's own."""
+    q = np.asarray(q, dtype=np.int8)
+    i = q.shape[0] // 2
+    gate, up = pack_weight(q[:i]), pack_weight(q[i:])
+    out = np.empty((2 * gate.shape[0],) + gate.shape[1:], np.int8)
+    out[0::2], out[1::2] = gate, up
+    return out
+
+
+def silu64(v: np.ndarray) -> np.ndarray:
+    """v * sigmoid(v) in fp64, written as v / (1 + e^-v) (e^-v overflowing to inf gives -0 for
+    very negative v, the limit)."""
+    v = np.asarray(v, np.float64)
+    with np.errstate(over="ignore"):
+        return v / (1.0 + np.exp(-v))
+
+
+def w8a16_glu_golden(x_bits: np.ndarray, q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """fp64 golden of h = silu(g) * u (M, I) for the stacked (2I, K) weight q and (2I,) scales s:
+    g = w8a16_golden over the gate half, u over the up half."""
+    i = np.asarray(q).shape[0] // 2
+    g = w8a16_golden(x_bits, q[:i], s[:i])
+    u = w8a16_golden(x_bits, q[i:], s[i:])
+    return silu64(g) * u
+
+
+def w8a8_glu_operands(acc: np.ndarray, sx: np.ndarray, s: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The fp32 gate and up values of the W8A8 gate/up epilogue from the exact int32 sums of the
+    stacked weight (M, 2I): (fp32(acc) * sx[m]) * s[n], two fp32 roundings, split in halves."""
+    a = np.asarray(acc, dtype=np.int32).astype(np.float32)
+    v = (a * np.asarray(sx, np.float32)[:, None]) * np.asarray(s, np.float32)[None, :]
+    i = v.shape[1] // 2
+    return v[:, :i].astype(np.float32), v[:, i:].astype(np.float32)
+
+
+def w8a8_glu_golden(acc: np.ndarray, sx: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """fp64 h = silu(g) * u from the exact fp32 g, u of `w8a8_glu_operands`; the kernel's
+    result is this value rounded once to bf16, up to the fp32 error of its SiLU."""
+    g, u = w8a8_glu_operands(acc, sx, s)
+    return silu64(g) * u.astype(np.float64)
+
+
+def bf16_ulps_apart(y_bits: np.ndarray, golden: np.ndarray) -> np.ndarray:
+    """|y - golden| in units of the bf16 spacing at golden (2^(e-7) for |golden| in [2^e,
+    2^(e+1)); the smallest normal spacing below that)."""
+    y = bf16_bits_to_f32(y_bits).astype(np.float64)
+    g = np.asarray(golden, np.float64)
+    _, e = np.frexp(np.maximum(np.abs(g), np.finfo(np.float32).tiny))
+    return np.abs(y - g) / np.ldexp(1.0, e - 8)

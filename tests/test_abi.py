@@ -153,3 +153,40 @@ def test_status_strings(pkg):
     lib = pkg.library()
     for st in (0, E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO, E_WORKSPACE, -99):
         assert isinstance(lib.lse_status_string(st), bytes)
+
+
+def test_glu_entry_points_reject_bad_arguments(pkg):
+    lib = pkg.library()
+    assert lib.lse_packed_glu_bytes(14336, 4096) == 2 * 896 * 64 * 1024
+    assert lib.lse_packed_glu_bytes(20, 80) == 2 * 2 * 2 * 1024
+    assert lib.lse_packed_glu_bytes(-1, 16) == -1
+    assert lib.lse_pack_glu(FAKE, 16, 40, FAKE, None) == E_ALIGN
+    assert lib.lse_pack_glu(FAKE, -1, 32, FAKE, None) == E_SHAPE
+    assert lib.lse_pack_glu(None, 16, 32, FAKE, None) == E_NULL
+    assert lib.lse_pack_glu(FAKE, 1 << 19, 4096, FAKE, None) == E_RANGE
+    assert lib.lse_pack_glu(None, 0, 32, None, None) == 0
+    # (x, ldx, qp, s, h, ldh, M, I, K, algo)
+    ok = (FAKE, 64, FAKE, FAKE, FAKE, 64, 2, 64, 64, 0)
+    cases = [
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 2, 64, 40, 0), E_ALIGN),
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 2, -1, 64, 0), E_SHAPE),
+        ((FAKE, 64, FAKE, FAKE, FAKE, 32, 2, 64, 64, 0), E_SHAPE),  # ldh < I
+        ((FAKE, 64, None, FAKE, FAKE, 64, 2, 64, 64, 0), E_NULL),
+        ((FAKE, 64, FAKE, None, FAKE, 64, 2, 64, 64, 0), E_NULL),
+        ((None, 64, FAKE, FAKE, FAKE, 64, 2, 64, 64, 0), E_NULL),
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 65, 64, 64, 1), E_ALGO),
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 2, 64, 64, 3), E_ALGO),
+        ((FAKE, 64, FAKE, FAKE, FAKE, 64, 2, 64, 200_000, 0), E_RANGE),
+        ((FAKE, 4096, FAKE, FAKE, FAKE, 1 << 19, 1, 1 << 19, 4096, 0), E_RANGE),
+        ((FAKE, 1 << 23, FAKE, FAKE, FAKE, 64, 100, 64, 64, 2), E_RANGE),
+    ]
+    for args, status in cases:
+        assert lib.lse_w8a16_glu(*args, None) == status, args
+    assert lib.lse_w8a16_glu(*ok[:6], 0, 64, 64, 0, None) == 0  # M = 0
+    # (xq, sx, qp, s, h, ldh, M, I, K)
+    assert lib.lse_w8a8_glu(FAKE, None, FAKE, FAKE, FAKE, 64, 2, 64, 64, None) == E_NULL
+    assert lib.lse_w8a8_glu(None, FAKE, FAKE, FAKE, FAKE, 64, 2, 64, 64, None) == E_NULL
+    assert lib.lse_w8a8_glu(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 2, 64, 200_000, None) == E_RANGE
+    assert lib.lse_w8a8_glu(ctypes.c_void_p((1 << 20) + 4), FAKE, FAKE, FAKE, FAKE, 64, 2, 64,
+                            64, None) == E_ALIGN
+    assert lib.lse_w8a8_glu(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 2, 64, 64, None) == E_SHAPE

@@ -103,8 +103,9 @@ def test_quantize_model_swaps_llama_projections(pkg, dev):
     for layer in model.model.layers:
         for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
             assert isinstance(getattr(layer.self_attn, name), pkg.Int8Linear)
-        for name in ("gate_proj", "up_proj", "down_proj"):
-            assert isinstance(getattr(layer.mlp, name), pkg.Int8Linear)
+        assert isinstance(layer.mlp, pkg.Int8GluMLP)
+        assert isinstance(layer.mlp.gate_up, pkg.Int8GateUp)
+        assert isinstance(layer.mlp.down_proj, pkg.Int8Linear)
     assert isinstance(model.lm_head, nn.Linear) and not isinstance(model.lm_head, pkg.Int8Linear)
     assert next(model.parameters()).dtype == torch.bfloat16
     with torch.no_grad():

@@ -100,3 +100,30 @@ def test_unpack_inverts_the_oracle_packing(pkg):
         qp = torch.from_numpy(ora.pack_weight(q))
         assert tuple(qp.shape) == pkg.ops.packed_shape(n, k)
         np.testing.assert_array_equal(pkg.ops.unpack_weight(qp, n, k).numpy(), q)
+
+
+def test_unpack_glu_inverts_the_oracle_packing(pkg):
+    import numpy as np
+
+    from oracle import numerics as ora
+
+    rng = np.random.default_rng(6)
+    for i, k in ((1, 16), (20, 80), (48, 256)):
+        q = rng.integers(-127, 128, (2 * i, k)).astype(np.int8)
+        qp = torch.from_numpy(ora.pack_glu(q))
+        assert tuple(qp.shape) == pkg.ops.packed_glu_shape(i, k)
+        np.testing.assert_array_equal(pkg.ops.unpack_glu(qp, i, k).numpy(), q)
+
+
+def test_mlp_fusion_eligibility(pkg):
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaMLP
+
+    from llm_serving_engine_amd.int8_linear import fusable_mlp
+
+    assert fusable_mlp(LlamaMLP(LlamaConfig(hidden_size=32, intermediate_size=64)))
+    assert not fusable_mlp(LlamaMLP(LlamaConfig(hidden_size=32, intermediate_size=64,
+                                                hidden_act="gelu")))
+    assert not fusable_mlp(LlamaMLP(LlamaConfig(hidden_size=32, intermediate_size=64,
+                                                mlp_bias=True)))
+    assert not fusable_mlp(nn.Linear(4, 4))

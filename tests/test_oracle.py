@@ -320,3 +320,77 @@ def test_pack_weight_feeds_the_tile_walk_that_the_kernels_do():
                 k0 = 64 * j + 16 * (lane // 16)
                 y[:, row] += x[:, k0:k0 + 16] @ tile[lane]
     np.testing.assert_array_equal(y, x @ q.astype(np.int64).T)
+
+
+# ---- fused gate/up -------------------------------------------------------------------------
+
+
+def test_silu64_matches_torch_silu_and_the_llama_act_fn():
+    """silu64 against torch.nn.functional.silu and transformers' SiLUActivation (the act_fn
+    LlamaMLP applies, modeling_llama.py:172,175), in fp64, including both tails."""
+    from transformers.activations import ACT2FN
+
+    v = np.concatenate([np.linspace(-60, 60, 4001), [-1000.0, -88.7, 0.0, 1e-30, 88.7, 1000.0]])
+    ours = ora.silu64(v)
+    t = torch.from_numpy(v)
+    np.testing.assert_allclose(ours, torch.nn.functional.silu(t).numpy(), rtol=1e-14, atol=1e-300)
+    np.testing.assert_allclose(ours, ACT2FN["silu"](t).numpy(), rtol=1e-14, atol=1e-300)
+    # closed forms: silu(0) = 0, silu(v) - silu(-v) = v
+    assert ours[np.argmax(v == 0.0)] == 0.0
+    np.testing.assert_allclose(ora.silu64(v) - ora.silu64(-v), v, rtol=1e-12, atol=1e-12)
+
+
+def test_glu_golden_is_llama_mlp_in_fp64():
+    """With K = I and down_proj set to the identity, transformers' own LlamaMLP in fp64 over the
+    dequantized weights computes exactly act_fn(gate(x)) * up(x), the golden's definition."""
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaMLP
+
+    k = i = 64
+    x_bits, w = ora.seeded_inputs(21, 5, 2 * i, k)
+    q, s = ora.quantize_weight_per_channel(w)
+    mlp = LlamaMLP(LlamaConfig(hidden_size=k, intermediate_size=i, hidden_act="silu")).double()
+    deq = torch.from_numpy(q.astype(np.float64) * s.astype(np.float64)[:, None])
+    with torch.no_grad():
+        mlp.gate_proj.weight.copy_(deq[:i])
+        mlp.up_proj.weight.copy_(deq[i:])
+        mlp.down_proj.weight.copy_(torch.eye(i, dtype=torch.float64))
+        ref = mlp(torch.from_numpy(ora.bf16_bits_to_f32(x_bits).astype(np.float64))).numpy()
+    np.testing.assert_allclose(ora.w8a16_glu_golden(x_bits, q, s), ref, rtol=1e-12, atol=1e-14)
+
+
+def test_pack_glu_matches_the_layout_definition_by_brute_force():
+    """Byte 16 l + b of tile (rb, j) is row (rb & 1) I + 16 (rb >> 1) + l % 16 of the stacked
+    weight at column 64 j + 16 (l // 16) + b, zero past I or K; ragged I and K."""
+    rng = np.random.default_rng(9)
+    i, k = 20, 80
+    q = rng.integers(-127, 128, (2 * i, k)).astype(np.int8)
+    qp = ora.pack_glu(q)
+    assert qp.shape == (4, 2, 1024)
+    for rb in range(4):
+        for j in range(2):
+            for lane in range(64):
+                for b in range(16):
+                    r = 16 * (rb >> 1) + lane % 16
+                    c = 64 * j + 16 * (lane // 16) + b
+                    want = q[(rb & 1) * i + r, c] if r < i and c < k else 0
+                    assert qp[rb, j, 16 * lane + b] == want, (rb, j, lane, b)
+
+
+def test_w8a8_glu_operands_are_the_pinned_epilogue_before_rounding():
+    """g and u rounded to bf16 are exactly the W8A8 epilogue of each half."""
+    x_bits, w = ora.seeded_inputs(4, 7, 2 * 48, 256, outliers=True)
+    q, s = ora.quantize_weight_per_channel(w)
+    xq, sx = ora.quantize_act_per_token(x_bits)
+    acc = ora.w8a8_accumulate(xq, q)
+    g, u = ora.w8a8_glu_operands(acc, sx, s)
+    np.testing.assert_array_equal(ora.f32_to_bf16_bits(g), ora.w8a8_epilogue(acc[:, :48], sx, s[:48]))
+    np.testing.assert_array_equal(ora.f32_to_bf16_bits(u), ora.w8a8_epilogue(acc[:, 48:], sx, s[48:]))
+    np.testing.assert_allclose(ora.w8a8_glu_golden(acc, sx, s),
+                               g / (1 + np.exp(-g.astype(np.float64))) * u, rtol=1e-15)
+
+
+def test_bf16_ulps_apart_known_answers():
+    ys = ora.f32_to_bf16_bits(np.array([1.0, 1.0078125, 3.0, -0.5, 0.0], np.float32))
+    gold = np.array([1.0, 1.0, 3.03125, -0.5, 0.0])
+    np.testing.assert_allclose(ora.bf16_ulps_apart(ys, gold), [0.0, 1.0, 2.0, 0.0, 0.0])
