@@ -8,8 +8,10 @@ streams its weights from HBM). value = algorithmic bytes (K·N + 4N + 2MK + 2MN 
 time, in GB/s.
 
 Secondary figures on the same line: config 2 (W8A16 prefill GEMM, TFLOP/s at M=2048 and the
-M sweep) and config 3 (W8A8 quantize + int8 GEMM, TOP/s), plus the roofline of the decode
-kernel and the CPU baseline (the reference's bf16 F.linear on the host cores).
+M sweep), config 3 (W8A8 quantize + int8 GEMM, TOP/s) and the fused gate_up + SiLU-mul kernels
+(decode GB/s, prefill TFLOP/s, each beside the unfused GEMM + SiLU-mul they replace), plus the
+roofline of the decode kernel and the CPU baseline (the reference's bf16 F.linear on the host
+cores).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-secondary]
 
@@ -50,6 +52,7 @@ CALIBRATION_BYTES = 64 << 20
 PROFILE_MD = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.md"
 PROFILE_TRAFFIC = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.traffic.json"
 PROFILE_PREFILL = REPO_ROOT / "profiles" / "tiled_gemm_kernel_prefill.md"
+PROFILE_GLU = REPO_ROOT / "profiles" / "fused_gate_up_kernels.md"
 CUS, SIMDS_PER_CU, XCDS = 256, 4, 8
 
 
@@ -64,10 +67,12 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true", help="skip prefill and W8A8 figures")
-    p.add_argument("--only", choices=["decode", "prefill", "w8a8", "decode-step"],
+    p.add_argument("--only", choices=["decode", "prefill", "w8a8", "glu", "decode-step"],
                    help="one family; decode-step is config 4 (a 32-layer model's decode step)")
     p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
                    help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
+    p.add_argument("--summarize-glu", metavar="TRACE",
+                   help="write the fused gate_up profile summary from a kernel trace of --only glu")
     p.add_argument("--summarize-prefill", nargs=2, metavar=("TRACE", "PMC"),
                    help="summarize rocprofv3 output dirs of --only prefill into profiles/")
     return p.parse_args()
@@ -227,6 +232,58 @@ def bench_w8a8(pkg, dev, steps: int, gen) -> dict:
 
         t = time_region(step, max(2, steps // 4), 1) / max(2, steps // 4)
         res[str(m)] = {"tops": round(ops / t / 1e12, 2), "ms": round(t * 1e3, 3)}
+    return res
+
+
+GLU_K, GLU_I = 4096, 14336  # Llama-3-8B gate/up: two (14336, 4096) weights
+
+
+def bench_glu(pkg, dev, steps: int, gen) -> dict:
+    """Fused gate_up + SiLU-mul at the Llama-3-8B shape: decode (M in DECODE_MS, over LAYERS weight
+    copies, graph-replayed) in GB/s of algorithmic bytes (2IK + 8I + 2MK + 2MI), prefill at
+    M = 2048 in TFLOP/s (4MIK), each beside the unfused pair it replaces (the stacked W8A16
+    GEMM, then torch's SiLU and product on its bf16 halves)."""
+    import torch
+
+    k, i = GLU_K, GLU_I
+    weights = []
+    for _ in range(LAYERS):
+        w = (torch.randn(2 * i, k, generator=gen, device="cpu") * 0.02).to(dev)
+        q, s = pkg.ops.quantize_weight_per_channel(w)
+        weights.append((pkg.ops.pack_glu(q), pkg.ops.pack_weight(q), s))
+        del w, q
+
+    def fused(x, qg, s):
+        pkg.ops.w8a16_glu(x, qg, s)
+
+    def unfused(x, qp, s):
+        gu = pkg.ops.w8a16_linear(x, qp, s)
+        torch.nn.functional.silu(gu[:, :i]) * gu[:, i:]
+
+    def graph_time(fn, xs, copies):
+        fn_all = lambda: [fn(xs, *c) for c in copies]  # noqa: E731
+        fn_all()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn_all()
+        return time_region(g.replay, steps, 1) / (steps * len(copies))
+
+    res = {"I": i, "K": k, "decode": {}}
+    for m in DECODE_MS:
+        x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+        t = graph_time(fused, x, [(qg, s) for qg, _, s in weights])
+        t0 = graph_time(unfused, x, [(qp, s) for _, qp, s in weights])
+        nbytes = 2 * i * k + 8 * i + 2 * m * k + 2 * m * i
+        res["decode"][str(m)] = {"us": round(t * 1e6, 2), "gbps": round(nbytes / t / 1e9, 1),
+                                 "unfused_us": round(t0 * 1e6, 2)}
+    m = 2048
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+    t = graph_time(fused, x, [(weights[0][0], weights[0][2])])
+    t0 = graph_time(unfused, x, [(weights[0][1], weights[0][2])])
+    res["prefill_M2048"] = {"us": round(t * 1e6, 1), "tflops": round(4 * m * i * k / t / 1e12, 1),
+                            "mfma_frac": round(4 * m * i * k / t / 1e12 / BF16_PEAK_TFLOPS, 4),
+                            "unfused_us": round(t0 * 1e6, 1)}
     return res
 
 
@@ -429,6 +486,48 @@ def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
     print("\n".join(out))
 
 
+def summarize_glu(trace_dir: str) -> None:
+    """Per-kernel durations of `bench.py --only glu` from a kernel trace: the fused kernels (last
+    template argument true) and the unfused GEMMs and elementwise kernels they replace, grouped
+    by kernel and grid (M = 1 and M = 8 share the M <= 16 kernel and grid)."""
+    import csv
+    import statistics
+
+    with open(Path(trace_dir) / "run_kernel_trace.csv", newline="") as f:
+        trace = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    groups: dict[tuple[str, int], list[float]] = {}
+    for r in trace:
+        name = r["Kernel_Name"]
+        kernels = ("skinny_kernel", "tiled_gemm_kernel", "silu", "BinaryFunctor")
+        if not any(t in name for t in kernels):
+            continue
+        short = name.split("(")[0].replace("void ", "").replace("lse::", "")
+        if "at::native" in short:
+            short = "torch silu" if "silu" in name else "torch mul"
+        key = (short, int(r["Grid_Size_X"]))
+        groups.setdefault(key, []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    cmds = [
+        "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_glu -o run --output-format csv -- "
+        "python3 bench.py --only glu --steps 5",
+        "python3 bench.py --summarize-glu gpurun_out/prof_glu",
+    ]
+    out = [f"# Fused gate_up + SiLU-mul kernels (I = {GLU_I}, K = {GLU_K}), one MI355X", "",
+           "Commands (repository root, one MI355X; the last runs on any host):", "", "```", *cmds,
+           "```", "",
+           "Fused kernels carry `true` as their last template argument; the unfused pair they "
+           "replace is the stacked GEMM (same kernel family, `false`) followed by torch's SiLU "
+           "and product on its bf16 halves. Decode launches rotate 8 weight copies (940 MB), so "
+           "every launch streams its weights from HBM. Durations are kernel-trace "
+           "end - start.", "",
+           "| kernel | grid | dispatches | median us | min us |", "|---|---|---|---|---|"]
+    for (short, grid), ds in sorted(groups.items(), key=lambda kv: (kv[0][0], kv[0][1])):
+        out.append(f"| `{short}` | {grid} | {len(ds)} | {statistics.median(ds):.2f} | "
+                   f"{min(ds):.2f} |")
+    PROFILE_GLU.write_text("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
 def collections_by_dispatch(rows: list[dict], kernel: str) -> list[dict]:
     """Counter rows of one --pmc run -> one {counter: value} dict per dispatch of `kernel`, in
     dispatch order."""
@@ -468,9 +567,11 @@ def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
     prefilled to `context` tokens by the bf16 model, then `decode_steps` teacher-forced decode
     steps with bf16 linears (the reference path) and with int8 W8A16 linears, from the same KV
     state. Reports the per-step linear time of each stack (replayed from a captured graph at
-    M = batch), aggregate HBM GB/s, the greedy next-token match rate against the bf16 reference
-    (limited by quantization: random-init logits are nearly flat) and against an eager torch
-    restatement of the same int8 weights (the kernels' own parity), and the top-2 logit margin."""
+    M = batch; both include the MLP's SiLU-mul, a separate call on bf16 and inside the fused
+    gate/up kernel on int8), aggregate HBM GB/s, the greedy next-token match rate against the
+    bf16 reference (limited by quantization: random-init logits are nearly flat) and against an
+    eager torch restatement of the same int8 weights (the kernels' own parity), and the top-2
+    logit margin."""
     import torch
 
     from llm_serving_engine_amd.decode_step import DecodeRunner, random_llama
@@ -548,6 +649,9 @@ def main() -> None:
     if args.summarize_prefill:
         summarize_prefill(*args.summarize_prefill)
         return
+    if args.summarize_glu:
+        summarize_glu(args.summarize_glu)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the int8 Linear "
               "path runs on a single MI355X; multi-GPU sharding is a design note only)",
@@ -572,6 +676,9 @@ def main() -> None:
     if args.only == "w8a8":
         print(json.dumps({"w8a8": bench_w8a8(pkg, dev, args.steps, gen)}))
         return
+    if args.only == "glu":
+        print(json.dumps({"fused_gate_up": bench_glu(pkg, dev, args.steps, gen)}))
+        return
     if args.only == "decode-step":
         print(json.dumps({"decode_step": bench_decode_step(pkg, dev, args.steps)}))
         return
@@ -580,6 +687,7 @@ def main() -> None:
     if not args.no_secondary and args.only is None:
         secondary["prefill_w8a16"] = bench_prefill(pkg, dev, args.steps, gen)
         secondary["w8a8"] = bench_w8a8(pkg, dev, args.steps, gen)
+        secondary["fused_gate_up"] = bench_glu(pkg, dev, args.steps, gen)
 
     cpu = None
     if not args.no_cpu and args.only is None:

@@ -130,7 +130,6 @@ skinny_kernel(SkinnyArgs a) {
   constexpr int RS1 = RS0 * W * 1024 <= kRedBudget ? RS0 : kRedBudget / (W * 1024);
   constexpr int RS = GLU ? RS1 & ~1 : RS1;
   static_assert(RS >= (GLU ? 2 : 1), "no LDS left for the cross-wave reduction");
-  constexpr int NPASS = (SLICES + RS - 1) / RS;
 
   __shared__ Acc red[W][RS][64];
   __shared__ float s_lds[kSkinnyScaleLds];
@@ -371,42 +370,57 @@ skinny_kernel(SkinnyArgs a) {
     store_glu4<I8>(a.y, a.ldy, m, n, cnt, vg, vu, sg, su, sxv[b], yvec);
   };
 
-  // End of a unit (panel p of split sp): pass i adds slices [i RS, i RS + RS) over the waves in
-  // wave order; wave w < RS keeps slice i RS + w and stores it (gate/up: wave w < RS / 2 keeps
-  // the pair i RS + 2 w, i RS + 2 w + 1).
-  auto unit_end = [&](int p, int sp) {
+  // Storage of the partial sums of a reduction pass: wave w's 1 KB of pass slice sl (all lanes'
+  // Acc) at slice_ptr(sl, w). Slices below RS live in `red`. In a workgroup's last unit the
+  // activation ring is idle (its remaining loads move no data), so slices from RS on take each
+  // wave's part of the ring slots, CPS per slot: one or two passes instead of up to eight.
+  constexpr int CPS = XLDS ? 0 : XWAVE / 64;
+  constexpr int RSW0 = RS + DX * CPS;
+  constexpr int RSW = GLU ? RSW0 & ~1 : RSW0;
+  auto slice_ptr = [&](int sl, int w) -> Acc* {
+    if (sl < RS) return &red[w][sl][0];
+    constexpr int cps = CPS > 0 ? CPS : 1;
+    const int j = (sl - RS) / cps, c = (sl - RS) % cps;
+    return reinterpret_cast<Acc*>(xslot(j) + w * XWAVE + 64 * c);
+  };
+
+  // End of a unit (panel p of split sp), with CAP slices of storage per pass: pass i adds slices
+  // [i CAP, i CAP + CAP) over the waves in wave order (the order does not depend on CAP); wave w
+  // keeps slices i CAP + w, i CAP + w + W, ... and stores them (gate/up: the pairs 2 w, 2 w + 1,
+  // 2 (w + W), ... of the pass).
+  auto unit_end = [&](int p, int sp, auto cap) {
+    constexpr int CAP = decltype(cap)::value;
+    constexpr int NP = (SLICES + CAP - 1) / CAP;
 #pragma unroll
-    for (int i = 0; i < NPASS; ++i) {
-      __syncthreads();  // the previous pass's (or panel's) reads of red are done
+    for (int i = 0; i < NP; ++i) {
+      __syncthreads();  // the previous pass's (or unit's) reads of the storage are done
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int b = 0; b < MT; ++b) {
-          const int sl = rt + RT * b - RS * i;
-          if (sl < 0 || sl >= RS) continue;
+          const int sl = rt + RT * b - CAP * i;
+          if (sl < 0 || sl >= CAP) continue;
           Acc v = acc[rt][b][0];
           if constexpr (NACC == 2) v += acc[rt][b][1];
-          red[wave][sl][lane] = v;
+          slice_ptr(sl, wave)[lane] = v;
         }
       __syncthreads();
       if constexpr (GLU) {
-        const int slice = 2 * wave + RS * i;
-        if (2 * wave < RS && slice < SLICES) {
-          Acc vg = red[0][2 * wave][lane], vu = red[0][2 * wave + 1][lane];
+        for (int sl = 2 * wave; sl < CAP && sl + CAP * i < SLICES; sl += 2 * W) {
+          Acc vg = slice_ptr(sl, 0)[lane], vu = slice_ptr(sl + 1, 0)[lane];
 #pragma unroll
           for (int w2 = 1; w2 < W; ++w2) {
-            vg += red[w2][2 * wave][lane];
-            vu += red[w2][2 * wave + 1][lane];
+            vg += slice_ptr(sl, w2)[lane];
+            vu += slice_ptr(sl + 1, w2)[lane];
           }
-          store_glu(p, slice, vg, vu);
+          store_glu(p, sl + CAP * i, vg, vu);
         }
       } else {
-        const int slice = wave + RS * i;
-        if (wave < RS && slice < SLICES) {
-          Acc v = red[0][wave][lane];
+        for (int sl = wave; sl < CAP && sl + CAP * i < SLICES; sl += W) {
+          Acc v = slice_ptr(sl, 0)[lane];
 #pragma unroll
-          for (int w2 = 1; w2 < W; ++w2) v += red[w2][wave][lane];
-          store_out(p, sp, slice, v);
+          for (int w2 = 1; w2 < W; ++w2) v += slice_ptr(sl, w2)[lane];
+          store_out(p, sp, sl + CAP * i, v);
         }
       }
     }
@@ -444,7 +458,14 @@ skinny_kernel(SkinnyArgs a) {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    unit_end(p, sp);
+    if constexpr (RSW > RS) {
+      if (u + 1 == u_end) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the ring's last loads have landed
+        unit_end(p, sp, std::integral_constant<int, RSW>{});
+        continue;
+      }
+    }
+    unit_end(p, sp, std::integral_constant<int, RS>{});
   }
 }
 

@@ -205,19 +205,23 @@ class DecodeRunner:
 
     def linear_calls(self, m: int) -> list:
         """(module, input) for every projection of one decode step at M = m, with inputs of the
-        right shapes (the values do not change the time of a weight stream)."""
+        right shapes (the values do not change the time of a weight stream), and the MLP's
+        SiLU-mul between gate/up and down: a call of its own on the bf16 back end, inside the
+        fused gate/up kernel on the int8 one."""
         dev = next(self.model.parameters()).device
         g = torch.Generator(device="cpu").manual_seed(7)
         hid = self.model.config.hidden_size
         inter = self.model.config.intermediate_size
         x_h = torch.randn(m, hid, generator=g).to(torch.bfloat16).to(dev)
         x_i = torch.randn(m, inter, generator=g).to(torch.bfloat16).to(dev)
+        x_gu = torch.randn(m, 2 * inter, generator=g).to(torch.bfloat16).to(dev)
         calls = []
         for i, layer in enumerate(self.layers):
             if self.backend == "bf16":
                 a, p = layer.self_attn, layer.mlp
                 calls += [(a.q_proj, x_h), (a.k_proj, x_h), (a.v_proj, x_h), (a.o_proj, x_h),
-                          (p.gate_proj, x_h), (p.up_proj, x_h), (p.down_proj, x_i)]
+                          (p.gate_proj, x_h), (p.up_proj, x_h), (SiluMul(p.act_fn), x_gu),
+                          (p.down_proj, x_i)]
             else:
                 d = self.int8[i]
                 calls += [(d["qkv"], x_h), (d["o"], x_h), (d["gate_up"], x_h), (d["down"], x_i)]
@@ -232,6 +236,8 @@ class DecodeRunner:
             if isinstance(mod, Int8GateUp):  # both weights in, the SiLU-mul product out
                 n = 2 * mod.intermediate_size
                 total += k * n + 4 * n + 2 * m * k + 2 * m * (n // 2)
+            elif isinstance(mod, SiluMul):  # (M, 2I) in, (M, I) out
+                total += 2 * m * k + m * k
             elif isinstance(mod, Int8Linear):
                 n = mod.out_features
                 total += k * n + 4 * n + 2 * m * k + 2 * m * n
@@ -239,6 +245,20 @@ class DecodeRunner:
                 n = mod.out_features
                 total += 2 * k * n + 2 * m * k + 2 * m * n
         return total
+
+
+class SiluMul(nn.Module):
+    """`act_fn(gate) * up` of LlamaMLP.forward (modeling_llama.py:175) on a stacked (..., 2I)
+    [gate | up] input, as a separate call (the bf16 back end's activation between gate/up and
+    down)."""
+
+    def __init__(self, act_fn: nn.Module) -> None:
+        super().__init__()
+        self.act_fn = act_fn
+
+    def forward(self, gu: torch.Tensor) -> torch.Tensor:
+        i = gu.shape[-1] // 2
+        return self.act_fn(gu[..., :i]) * gu[..., i:]
 
 
 def _int8(weight: torch.Tensor, mode: str) -> Int8Linear:

@@ -214,5 +214,6 @@ class Int8GluMLP(nn.Module):
 def fusable_mlp(mlp: nn.Module) -> bool:
     """Whether `mlp` has the LlamaMLP form the fused gate/up kernel computes."""
     parts = [getattr(mlp, n, None) for n in ("gate_proj", "up_proj", "down_proj")]
-    return (all(isinstance(p, nn.Linear) for p in parts) and _is_silu(getattr(mlp, "act_fn", None))
+    return (all(isinstance(p, nn.Linear) for p in parts)
+            and _is_silu(getattr(mlp, "act_fn", None))
             and parts[0].bias is None and parts[1].bias is None)
