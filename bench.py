@@ -53,6 +53,7 @@ PROFILE_MD = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.md"
 PROFILE_TRAFFIC = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.traffic.json"
 PROFILE_PREFILL = REPO_ROOT / "profiles" / "tiled_gemm_kernel_prefill.md"
 PROFILE_GLU = REPO_ROOT / "profiles" / "fused_gate_up_kernels.md"
+PROFILE_ATTN = REPO_ROOT / "profiles" / "paged_attn_kernel_decode.md"
 CUS, SIMDS_PER_CU, XCDS = 256, 4, 8
 
 
@@ -67,10 +68,14 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true", help="skip prefill and W8A8 figures")
-    p.add_argument("--only", choices=["decode", "prefill", "w8a8", "glu", "decode-step"],
+    p.add_argument("--only", choices=["decode", "prefill", "w8a8", "glu", "attention",
+                                      "decode-step"],
                    help="one family; decode-step is config 4 (a 32-layer model's decode step)")
     p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
                    help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
+    p.add_argument("--summarize-attention", metavar="TRACE",
+                   help="write the paged attention profile summary from a kernel trace of "
+                        "--only attention")
     p.add_argument("--summarize-glu", metavar="TRACE",
                    help="write the fused gate_up profile summary from a kernel trace of --only glu")
     p.add_argument("--summarize-prefill", nargs=2, metavar=("TRACE", "PMC"),
@@ -284,6 +289,68 @@ def bench_glu(pkg, dev, steps: int, gen) -> dict:
     res["prefill_M2048"] = {"us": round(t * 1e6, 1), "tflops": round(4 * m * i * k / t / 1e12, 1),
                             "mfma_frac": round(4 * m * i * k / t / 1e12 / BF16_PEAK_TFLOPS, 4),
                             "unfused_us": round(t0 * 1e6, 1)}
+    return res
+
+
+ATTN_CASES = [  # (name, entries, context, pools rotated)
+    ("decode_b64_ctx1025", 64, 1025, 4),    # config 4's decode step, one layer
+    ("decode_b8_ctx8192", 8, 8192, 4),      # few sequences, long context: the split path
+    ("decode_b256_ctx512", 256, 512, 4),
+]
+ATTN_H, ATTN_HKV, ATTN_D, ATTN_BS = 32, 8, 128, 16
+
+
+def bench_attention(pkg, dev, steps: int, gen) -> dict:
+    """Paged decode attention (one query token per sequence, Llama-3-8B heads, block size 16,
+    physical blocks shuffled over the pool): us per call and GB/s of algorithmic bytes (K and V
+    rows of every visible position, q in, o out, block table), over `pools` distinct pools so
+    each call streams its K/V from HBM; beside it torch's scaled_dot_product_attention on the
+    same K/V laid out contiguously (bf16, no paging)."""
+    import torch
+
+    res = {}
+    h, h_kv, d, bs = ATTN_H, ATTN_HKV, ATTN_D, ATTN_BS
+    for name, e, ctx, pools in ATTN_CASES:
+        nblk = -(-ctx // bs)
+        blocks = e * nblk + 1
+        perm = torch.randperm(blocks - 1, generator=gen)
+        table = perm[: e * nblk].reshape(e, nblk).to(torch.int32).to(dev)
+        kv = [(torch.randn(blocks, bs, h_kv, d, generator=gen).to(torch.bfloat16).to(dev),
+               torch.randn(blocks, bs, h_kv, d, generator=gen).to(torch.bfloat16).to(dev))
+              for _ in range(pools)]
+        q = torch.randn(h, e, d, generator=gen).to(torch.bfloat16).to(dev)
+        i32 = lambda v: torch.tensor(v, dtype=torch.int32, device=dev)  # noqa: E731
+        ctx_t, qo_t = i32([ctx] * e), i32([ctx - 1] * e)
+        qs_t, ql_t = i32(list(range(e))), i32([1] * e)
+
+        def step(kv=kv, q=q, table=table, ctx_t=ctx_t, qo_t=qo_t, qs_t=qs_t, ql_t=ql_t):
+            for kp, vp in kv:
+                pkg.ops.paged_attention_forward(q, kp, vp, table, ctx_t, qo_t, qs_t, ql_t, bs, 1)
+
+        step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        t = time_region(g.replay, steps, 1) / (steps * pools)
+        nbytes = e * ctx * h_kv * d * 2 * 2 + 2 * (h * e * d * 2) + e * nblk * 4
+        # torch SDPA on contiguous (E, H_KV, ctx, D) K/V, GQA by expansion to H heads
+        kc = torch.randn(e, h_kv, ctx, d, generator=gen).to(torch.bfloat16).to(dev)
+        vc = torch.randn(e, h_kv, ctx, d, generator=gen).to(torch.bfloat16).to(dev)
+        qc = q.permute(1, 0, 2).reshape(e, h, 1, d).contiguous()
+
+        def sdpa(kc=kc, vc=vc, qc=qc):
+            torch.nn.functional.scaled_dot_product_attention(
+                qc, kc, vc, enable_gqa=True)
+
+        sdpa()
+        torch.cuda.synchronize()
+        t0 = time_region(sdpa, steps, 2) / steps
+        res[name] = {"entries": e, "context": ctx, "us": round(t * 1e6, 2),
+                     "gbps": round(nbytes / t / 1e9, 1), "frac_of_8TBs": round(nbytes / t / 8e12, 4),
+                     "torch_sdpa_contiguous_us": round(t0 * 1e6, 2)}
+        del kv, kc, vc
+        torch.cuda.empty_cache()
     return res
 
 
@@ -528,6 +595,50 @@ def summarize_glu(trace_dir: str) -> None:
     print("\n".join(out))
 
 
+def summarize_attention(trace_dir: str) -> None:
+    """Kernel-trace durations of `bench.py --only attention`: the paged_attn_kernel dispatches,
+    in order, fall into one equal run per ATTN_CASES entry (each case dispatches the same
+    count); paged_attn_merge runs only for split cases and is matched to them by time."""
+    import csv
+    import statistics
+
+    with open(Path(trace_dir) / "run_kernel_trace.csv", newline="") as f:
+        trace = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    main = [r for r in trace if "paged_attn_kernel" in r["Kernel_Name"]]
+    merge = [r for r in trace if "paged_attn_merge" in r["Kernel_Name"]]
+    per = len(main) // len(ATTN_CASES)
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
+    h, h_kv, d, bs = ATTN_H, ATTN_HKV, ATTN_D, ATTN_BS
+    cmds = [
+        "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_att -o run --output-format csv -- "
+        "python3 bench.py --only attention --steps 5",
+        "python3 bench.py --summarize-attention gpurun_out/prof_att",
+    ]
+    out = ["# paged_attn_kernel — decode attention over a paged K/V pool, one MI355X", "",
+           "Commands (repository root, one MI355X; the last runs on any host):", "", "```", *cmds,
+           "```", "",
+           f"Llama-3-8B heads (H = {h}, H_KV = {h_kv}, D = {d}), block size {bs}, one query token "
+           "per sequence, physical blocks shuffled over the pool, 4 pools rotated so each call "
+           "streams its K/V from HBM. Algorithmic bytes = K and V rows of every visible position "
+           "+ q + o + block table. Durations are kernel-trace end - start (median); a split case "
+           "adds its paged_attn_merge pass.", "",
+           "| case | sequences | context | grid | kernel us | merge us | algorithmic MB | GB/s | "
+           "frac of 8 TB/s |", "|---|---|---|---|---|---|---|---|---|"]
+    for ci, (name, e, ctx, _pools) in enumerate(ATTN_CASES):
+        block = main[ci * per:(ci + 1) * per]
+        t0, t1 = int(block[0]["Start_Timestamp"]), int(block[-1]["End_Timestamp"])
+        ms = [dur(r) for r in merge if t0 <= int(r["Start_Timestamp"]) <= t1 + 1_000_000]
+        us = statistics.median(dur(r) for r in block)
+        mus = statistics.median(ms) if ms else 0.0
+        nblk = -(-ctx // bs)
+        nbytes = e * ctx * h_kv * d * 4 + 4 * h * e * d + 4 * e * nblk
+        gbps = nbytes / ((us + mus) * 1e3)
+        out.append(f"| {name} | {e} | {ctx} | {block[0]['Grid_Size_X']} | {us:.2f} | "
+                   f"{mus:.2f} | {nbytes / 1e6:.1f} | {gbps:.0f} | {gbps / 8000:.3f} |")
+    PROFILE_ATTN.write_text("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
 def collections_by_dispatch(rows: list[dict], kernel: str) -> list[dict]:
     """Counter rows of one --pmc run -> one {counter: value} dict per dispatch of `kernel`, in
     dispatch order."""
@@ -652,6 +763,9 @@ def main() -> None:
     if args.summarize_glu:
         summarize_glu(args.summarize_glu)
         return
+    if args.summarize_attention:
+        summarize_attention(args.summarize_attention)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the int8 Linear "
               "path runs on a single MI355X; multi-GPU sharding is a design note only)",
@@ -679,6 +793,9 @@ def main() -> None:
     if args.only == "glu":
         print(json.dumps({"fused_gate_up": bench_glu(pkg, dev, args.steps, gen)}))
         return
+    if args.only == "attention":
+        print(json.dumps({"paged_attention": bench_attention(pkg, dev, args.steps, gen)}))
+        return
     if args.only == "decode-step":
         print(json.dumps({"decode_step": bench_decode_step(pkg, dev, args.steps)}))
         return
@@ -688,6 +805,7 @@ def main() -> None:
         secondary["prefill_w8a16"] = bench_prefill(pkg, dev, args.steps, gen)
         secondary["w8a8"] = bench_w8a8(pkg, dev, args.steps, gen)
         secondary["fused_gate_up"] = bench_glu(pkg, dev, args.steps, gen)
+        secondary["paged_attention"] = bench_attention(pkg, dev, args.steps, gen)
 
     cpu = None
     if not args.no_cpu and args.only is None:

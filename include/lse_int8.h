@@ -76,7 +76,7 @@ enum lse_query_key {
   LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
 };
 
-#define LSE_ABI_VERSION 4
+#define LSE_ABI_VERSION 5
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -196,6 +196,49 @@ int lse_w8a16_glu(const void* x, int64_t ldx, const int8_t* qp, const float* s, 
  */
 int lse_w8a8_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* h,
                  int64_t ldh, int64_t M, int64_t I, int64_t K, void* stream);
+
+/*
+ * Bytes of device workspace (16-byte aligned) lse_paged_attention needs for these sizes on the
+ * current device: 0 when every (entry, K/V head, query tile) takes its whole context in one
+ * workgroup, the partial results of the key partitions otherwise. -1 for invalid sizes.
+ * Replaces: nothing in the reference (its Triton launch needs no scratch).
+ */
+int64_t lse_paged_attention_workspace_bytes(int64_t entries, int64_t H, int64_t H_KV, int64_t D,
+                                            int64_t max_q_len, int64_t max_blocks,
+                                            int64_t block_size);
+
+/*
+ * Paged attention of a whole batch plan at one layer against a shared K/V pool. For entry e,
+ * query row m < q_len[e] (q row q_start[e] + m, cache position query_offset[e] + m) and head h:
+ *   o[h][q_start[e] + m] = sum_n softmax_n(softmax_scale * q[h][q_start[e] + m] . k_n) v_n
+ * over cache positions n < context_len[e] with n <= query_offset[e] + m, where position n of
+ * entry e lives in pool block block_table[e][n / block_size], slot n % block_size, K/V head
+ * h / (H / H_KV). fp32 online softmax; probabilities rounded to bf16 before the product with V;
+ * bf16 output (a row with no position is written as zeros).
+ * q, o: bf16, element (h, t, d) at h * stride_h + t * stride_t + d. k_pool, v_pool: bf16
+ *   (blocks, block_size, H_KV, D), element (b, w, kh, d) at b * pool_stride_block +
+ *   w * pool_stride_slot + kh * pool_stride_head + d (the same strides for both).
+ * block_table: (entries, >= max_blocks) int32, row stride block_table_stride; context_len,
+ *   query_offset, q_start, q_len: (entries) int32. Their values must describe positions inside
+ *   the pool and rows inside q/o (the kernel reads only blocks the table names for positions
+ *   below context_len), as for the reference kernel.
+ * Shapes: D = 128; H a multiple of H_KV with H / H_KV in {1, 2, 4, 8, 16}; strides multiples of 8
+ *   elements and base pointers 16-byte aligned. max_q_len >= every q_len (a graphed decode may
+ *   pass its bucket size). workspace as sized by lse_paged_attention_workspace_bytes.
+ * Replaces: `paged_attention_forward` (src/llm_serving_engine/kernels/flash_attention.py:
+ *   287-332, the Triton kernel `paged_attention_2` at :201-284), called from
+ *   `ModelRunner.attend_paged` (model_runner.py:357-363).
+ */
+int lse_paged_attention(const void* q, int64_t q_stride_h, int64_t q_stride_t,
+                        const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                        int64_t pool_stride_slot, int64_t pool_stride_head,
+                        const int32_t* block_table, int64_t block_table_stride,
+                        const int32_t* context_len, const int32_t* query_offset,
+                        const int32_t* q_start, const int32_t* q_len, void* o,
+                        int64_t o_stride_h, int64_t o_stride_t, int64_t entries, int64_t H,
+                        int64_t H_KV, int64_t D, int64_t block_size, int64_t max_blocks,
+                        int64_t max_q_len, float softmax_scale, void* workspace,
+                        int64_t workspace_bytes, void* stream);
 
 /* Static properties (enum lse_query_key); -1 for an unknown key. Load-time checks read these,
  * as `ModelRunner.check_custom_kernel_support` (model_runner.py:77-94) checks its kernels. */

@@ -31,6 +31,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lse_pack_glu": (_INT, [_P, _I64, _I64, _P, _P]),
     "lse_w8a16_glu": (_INT, [_P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]),
     "lse_w8a8_glu": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "lse_paged_attention_workspace_bytes": (_I64, [_I64] * 7),
+    "lse_paged_attention": (_INT, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P,
+                                   _P, _P, _I64, _I64] + [_I64] * 7 + [ctypes.c_float, _P, _I64,
+                                                                        _P]),
     "lse_query": (_I64, [_INT]),
     "lse_status_string": (ctypes.c_char_p, [_INT]),
 }
@@ -41,7 +45,7 @@ ALGO_AUTO, ALGO_DECODE, ALGO_PREFILL = 0, 1, 2
 MODE_W8A16, MODE_W8A8 = 0, 1
 E_WORKSPACE = -6
 Q_ABI_VERSION, Q_K_ALIGN, Q_DECODE_MAX_M, Q_MAX_K, Q_GFX_ARCH = 0, 1, 2, 3, 4
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

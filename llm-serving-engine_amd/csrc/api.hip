@@ -40,6 +40,16 @@ int launch_w8a16_gemm_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, cons
 int launch_w8a8_gemm_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
                          uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
                          hipStream_t stream);
+int64_t paged_attention_workspace_bytes(int64_t entries, int64_t H, int64_t HKV, int64_t D,
+                                        int64_t max_q_len, int64_t max_ctx);
+int launch_paged_attention(const uint16_t* q, int64_t sq_h, int64_t sq_t, const uint16_t* k_pool,
+                           const uint16_t* v_pool, int64_t sb, int64_t sw, int64_t sh,
+                           const int32_t* block_table, int64_t sbt, const int32_t* context_len,
+                           const int32_t* query_offset, const int32_t* q_start,
+                           const int32_t* q_len, uint16_t* o, int64_t so_h, int64_t so_t,
+                           int64_t entries, int64_t H, int64_t HKV, int64_t block_size,
+                           int64_t max_blocks, int64_t max_q_len, float softmax_scale, void* ws,
+                           int64_t ws_bytes, hipStream_t stream);
 }  // namespace lse
 
 namespace lse {
@@ -299,6 +309,69 @@ int lse_w8a8_glu(const int8_t* xq, const float* sx, const int8_t* qp, const floa
   }
   if (256 * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
   return lse::launch_w8a8_gemm_glu(xq, sx, qp, s, (uint16_t*)h, ldh, M, I, K, st);
+}
+
+namespace {
+
+// Sizes lse_paged_attention accepts (see include/lse_int8.h).
+int check_attention_sizes(int64_t entries, int64_t H, int64_t HKV, int64_t D, int64_t max_q_len,
+                          int64_t max_blocks, int64_t block_size) {
+  if (entries < 0 || H < 1 || HKV < 1 || max_q_len < 0 || max_blocks < 0 || block_size < 1 ||
+      entries > kMaxRows || H > 65536 || max_q_len > kMaxRows)
+    return LSE_E_SHAPE;
+  if (D != 128 || H % HKV) return LSE_E_SHAPE;
+  const int64_t g = H / HKV;
+  if (g != 1 && g != 2 && g != 4 && g != 8 && g != 16) return LSE_E_SHAPE;
+  if (max_blocks * block_size > kMaxRows) return LSE_E_RANGE;
+  return LSE_OK;
+}
+
+}  // namespace
+
+int64_t lse_paged_attention_workspace_bytes(int64_t entries, int64_t H, int64_t H_KV, int64_t D,
+                                            int64_t max_q_len, int64_t max_blocks,
+                                            int64_t block_size) {
+  if (check_attention_sizes(entries, H, H_KV, D, max_q_len, max_blocks, block_size)) return -1;
+  if (entries == 0 || max_q_len == 0) return 0;
+  return lse::paged_attention_workspace_bytes(entries, H, H_KV, D, max_q_len,
+                                              max_blocks * block_size);
+}
+
+int lse_paged_attention(const void* q, int64_t q_stride_h, int64_t q_stride_t,
+                        const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                        int64_t pool_stride_slot, int64_t pool_stride_head,
+                        const int32_t* block_table, int64_t block_table_stride,
+                        const int32_t* context_len, const int32_t* query_offset,
+                        const int32_t* q_start, const int32_t* q_len, void* o,
+                        int64_t o_stride_h, int64_t o_stride_t, int64_t entries, int64_t H,
+                        int64_t H_KV, int64_t D, int64_t block_size, int64_t max_blocks,
+                        int64_t max_q_len, float softmax_scale, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
+  if (int st = check_attention_sizes(entries, H, H_KV, D, max_q_len, max_blocks, block_size))
+    return st;
+  if (entries == 0 || max_q_len == 0) return LSE_OK;
+  if (!q || !k_pool || !v_pool || !block_table || !context_len || !query_offset || !q_start ||
+      !q_len || !o)
+    return LSE_E_NULL;
+  if (q_stride_h < 0 || q_stride_t < 0 || o_stride_h < 0 || o_stride_t < 0 ||
+      pool_stride_block < 0 || pool_stride_slot < 0 || pool_stride_head < 0 ||
+      block_table_stride < max_blocks)
+    return LSE_E_SHAPE;
+  const int64_t strides[] = {q_stride_h, q_stride_t, o_stride_h, o_stride_t, pool_stride_block,
+                             pool_stride_slot, pool_stride_head};
+  for (int64_t s : strides)
+    if (s % 8) return LSE_E_ALIGN;
+  if (!aligned(q, 16) || !aligned(o, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) ||
+      !aligned(block_table, 4) || !aligned(context_len, 4) || !aligned(query_offset, 4) ||
+      !aligned(q_start, 4) || !aligned(q_len, 4))
+    return LSE_E_ALIGN;
+  if (workspace_bytes < 0 || (workspace && !aligned(workspace, 16))) return LSE_E_WORKSPACE;
+  return lse::launch_paged_attention(
+      (const uint16_t*)q, q_stride_h, q_stride_t, (const uint16_t*)k_pool,
+      (const uint16_t*)v_pool, pool_stride_block, pool_stride_slot, pool_stride_head, block_table,
+      block_table_stride, context_len, query_offset, q_start, q_len, (uint16_t*)o, o_stride_h,
+      o_stride_t, entries, H, H_KV, block_size, max_blocks, max_q_len, softmax_scale, workspace,
+      workspace_bytes, (hipStream_t)stream);
 }
 
 int64_t lse_query(int key) {

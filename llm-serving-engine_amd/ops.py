@@ -17,6 +17,7 @@ import torch
 from . import _lib
 
 __all__ = [
+    "paged_attention_forward",
     "pack_glu",
     "pack_weight",
     "packed_glu_shape",
@@ -298,3 +299,56 @@ def w8a8_glu(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor) -> torch.T
         "lse_w8a8_glu",
     )
     return h.view(*x.shape[:-1], i)
+
+
+def paged_attention_forward(
+    q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+    block_table: torch.Tensor, context_len: torch.Tensor, query_offset: torch.Tensor,
+    q_start: torch.Tensor, q_len: torch.Tensor, block_size: int, max_q_len: int,
+) -> torch.Tensor:
+    """One launch for a whole batch plan's attention at one layer against a shared paged K/V
+    pool, with the reference's signature and meaning (`paged_attention_forward`,
+    src/llm_serving_engine/kernels/flash_attention.py:287-332).
+
+    q: (H, total_tokens, D) bf16. k_pool/v_pool: (num_blocks, block_size, H_KV, D) bf16, already
+    holding this call's tokens. block_table (entries, max_blocks), context_len, query_offset,
+    q_start, q_len (entries,): int32 on the device. max_q_len >= every q_len. Returns o like q.
+    Softmax scale 1/sqrt(D). D = 128 and H / H_KV in {1, 2, 4, 8, 16}."""
+    dev = _on_gpu(q, k_pool, v_pool, block_table, context_len, query_offset, q_start, q_len)
+    _require(q.dim() == 3 and k_pool.dim() == 4 and v_pool.shape == k_pool.shape,
+             "q must be (H, T, D), k_pool/v_pool (num_blocks, block_size, H_KV, D)")
+    _require(q.dtype == k_pool.dtype == v_pool.dtype == torch.bfloat16,
+             f"paged attention runs on bf16 q/k/v, got {q.dtype}, {k_pool.dtype}, {v_pool.dtype}")
+    for name, t in (("block_table", block_table), ("context_len", context_len),
+                    ("query_offset", query_offset), ("q_start", q_start), ("q_len", q_len)):
+        _require(t.dtype == torch.int32, f"{name} must be int32, got {t.dtype}")
+    _require(block_table.dim() == 2 and block_table.stride(1) == 1, "block_table must be (E, B) "
+             "with unit column stride")
+    entries = block_table.shape[0]
+    for name, t in (("context_len", context_len), ("query_offset", query_offset),
+                    ("q_start", q_start), ("q_len", q_len)):
+        _require(t.dim() == 1 and t.shape[0] == entries and t.stride(0) == 1,
+                 f"{name} must be a contiguous ({entries},) tensor")
+    h, _tokens, d = q.shape
+    _, bs, h_kv, dk = k_pool.shape
+    _require(dk == d and bs == block_size, "pool shape does not match q / block_size")
+    _require(q.stride(2) == 1 and k_pool.stride(3) == 1 and v_pool.stride() == k_pool.stride(),
+             "head dim must be contiguous and k_pool/v_pool must share strides")
+    o = torch.empty_like(q)
+    lib = _lib.library()
+    nbytes = lib.lse_paged_attention_workspace_bytes(entries, h, h_kv, d, max_q_len,
+                                                     block_table.shape[1], block_size)
+    _require(nbytes >= 0, f"unsupported attention shape: H={h} H_KV={h_kv} D={d}")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
+    _lib.check(
+        lib.lse_paged_attention(
+            q.data_ptr(), q.stride(0), q.stride(1), k_pool.data_ptr(), v_pool.data_ptr(),
+            k_pool.stride(0), k_pool.stride(1), k_pool.stride(2), block_table.data_ptr(),
+            block_table.stride(0), context_len.data_ptr(), query_offset.data_ptr(),
+            q_start.data_ptr(), q_len.data_ptr(), o.data_ptr(), o.stride(0), o.stride(1),
+            entries, h, h_kv, d, block_size, block_table.shape[1], max_q_len, 1.0 / d ** 0.5,
+            *_ws_args(ws), _stream(dev),
+        ),
+        "lse_paged_attention",
+    )
+    return o

@@ -220,3 +220,69 @@ def bf16_ulps_apart(y_bits: np.ndarray, golden: np.ndarray) -> np.ndarray:
     g = np.asarray(golden, np.float64)
     _, e = np.frexp(np.maximum(np.abs(g), np.finfo(np.float32).tiny))
     return np.abs(y - g) / np.ldexp(1.0, e - 8)
+
+
+# ---- paged attention (the reference's paged_attention_forward) ------------------------------
+
+
+def paged_attention_golden(
+    q_bits: np.ndarray, k_pool_bits: np.ndarray, v_pool_bits: np.ndarray,
+    block_table: np.ndarray, context_len: np.ndarray, query_offset: np.ndarray,
+    q_start: np.ndarray, q_len: np.ndarray, block_size: int, scale: float | None = None,
+) -> tuple[np.ndarray, np.ndarray]:
+    """fp64 golden of paged attention (src/llm_serving_engine/kernels/flash_attention.py:201-284):
+    q (H, T, D) bf16 bits, pools (blocks, block_size, H_KV, D) bf16 bits. Entry e's query row m
+    (q row q_start[e] + m, cache position query_offset[e] + m) of head h attends to positions
+    n < context_len[e], n <= query_offset[e] + m, held at pool block block_table[e][n //
+    block_size], slot n % block_size, K/V head h // (H // H_KV); softmax of scale * q.k (scale
+    1/sqrt(D) by default) times V. Returns (o (H, T, D) fp64, covered (T,) bool): rows no entry
+    covers stay zero and are flagged False."""
+    q = bf16_bits_to_f32(q_bits).astype(np.float64)
+    kp = bf16_bits_to_f32(k_pool_bits).astype(np.float64)
+    vp = bf16_bits_to_f32(v_pool_bits).astype(np.float64)
+    h_all, t_all, d = q.shape
+    g = h_all // kp.shape[2]
+    scale = 1.0 / np.sqrt(d) if scale is None else scale
+    out = np.zeros_like(q)
+    covered = np.zeros(t_all, bool)
+    for e in range(len(q_len)):
+        ctx, qo, qs, ql = int(context_len[e]), int(query_offset[e]), int(q_start[e]), int(q_len[e])
+        if ql == 0:
+            continue
+        pos = np.arange(ctx)
+        blocks = np.asarray(block_table[e])[pos // block_size]
+        k = kp[blocks, pos % block_size]  # (ctx, H_KV, D)
+        v = vp[blocks, pos % block_size]
+        rows = np.arange(ql)
+        allowed = pos[None, :] <= (qo + rows)[:, None]  # (ql, ctx)
+        covered[qs:qs + ql] = True
+        for h in range(h_all):
+            s = scale * (q[h, qs:qs + ql] @ k[:, h // g].T)
+            s = np.where(allowed, s, -np.inf)
+            mx = np.max(s, axis=1, keepdims=True)
+            mx = np.where(np.isfinite(mx), mx, 0.0)
+            p = np.exp(s - mx)
+            den = p.sum(axis=1, keepdims=True)
+            out[h, qs:qs + ql] = np.where(den > 0, (p @ v[:, h // g]) / np.where(den > 0, den, 1),
+                                          0.0)
+    return out, covered
+
+
+def attention_within_tolerance(o_bits: np.ndarray, golden: np.ndarray, v_absmax: float,
+                               covered: np.ndarray | None = None) -> tuple[bool, str]:
+    """The paged-attention acceptance rule: |o - golden| <= 2^-8 (max|V| + |golden|) elementwise.
+    Rounding each probability to bf16 before the product with V moves the output by at most
+    2^-9 max|V| (it is a convex combination of V rows), and the bf16 output by 2^-9 |golden|:
+    the bound leaves a factor of two."""
+    o = bf16_bits_to_f32(o_bits).astype(np.float64)
+    g = np.asarray(golden, np.float64)
+    if covered is not None:
+        o, g = o[:, covered], g[:, covered]
+    if g.size == 0:
+        return True, "empty"
+    if not np.all(np.isfinite(o)):
+        return False, "non-finite output"
+    err = np.abs(o - g)
+    bound = 2.0 ** -8 * (v_absmax + np.abs(g))
+    worst = float(np.max(err / bound))
+    return worst <= 1.0, f"max err {float(err.max()):.3e}, worst err/bound {worst:.3f}"

@@ -394,3 +394,105 @@ def test_bf16_ulps_apart_known_answers():
     ys = ora.f32_to_bf16_bits(np.array([1.0, 1.0078125, 3.0, -0.5, 0.0], np.float32))
     gold = np.array([1.0, 1.0, 3.03125, -0.5, 0.0])
     np.testing.assert_allclose(ora.bf16_ulps_apart(ys, gold), [0.0, 1.0, 2.0, 0.0, 0.0])
+
+
+# ---- paged attention -----------------------------------------------------------------------
+
+
+def _paged_case(seed, h=8, h_kv=2, d=16, block_size=5, entries=((9, 0, 9), (1, 12, 13), (4, 3, 7))):
+    """(q_len, query_offset, context_len) per entry; shuffled physical blocks, one pool."""
+    rng = np.random.default_rng(seed)
+    q_len = np.array([e[0] for e in entries], np.int32)
+    qo = np.array([e[1] for e in entries], np.int32)
+    ctx = np.array([e[2] for e in entries], np.int32)
+    q_start = np.concatenate([[0], np.cumsum(q_len)[:-1]]).astype(np.int32)
+    nblk = [-(-c // block_size) for c in ctx]
+    perm = rng.permutation(sum(nblk) + 3)
+    table = np.zeros((len(entries), max(nblk)), np.int32)
+    at = 0
+    for e, n in enumerate(nblk):
+        table[e, :n] = perm[at:at + n]
+        at += n
+    blocks = len(perm)
+    tokens = int(q_len.sum())
+    q = ora.f32_to_bf16_bits(rng.standard_normal((h, tokens, d), dtype=np.float32))
+    kp = ora.f32_to_bf16_bits(rng.standard_normal((blocks, block_size, h_kv, d), dtype=np.float32))
+    vp = ora.f32_to_bf16_bits(rng.standard_normal((blocks, block_size, h_kv, d), dtype=np.float32))
+    return q, kp, vp, table, ctx, qo, q_start, q_len, block_size
+
+
+def test_paged_attention_golden_matches_torch_sdpa():
+    """Against torch's scaled_dot_product_attention in fp64 on each entry's gathered K/V with an
+    explicit causal-offset mask (an independent implementation of the same attention)."""
+    q, kp, vp, table, ctx, qo, qs, ql, bs = _paged_case(1)
+    out, covered = ora.paged_attention_golden(q, kp, vp, table, ctx, qo, qs, ql, bs)
+    assert covered.all()
+    qf = torch.from_numpy(ora.bf16_bits_to_f32(q).astype(np.float64))
+    kf = torch.from_numpy(ora.bf16_bits_to_f32(kp).astype(np.float64))
+    vf = torch.from_numpy(ora.bf16_bits_to_f32(vp).astype(np.float64))
+    g = qf.shape[0] // kf.shape[2]
+    for e in range(len(ql)):
+        pos = torch.arange(int(ctx[e]))
+        blk = torch.from_numpy(table[e].astype(np.int64))[pos // bs]
+        k = kf[blk, pos % bs].permute(1, 0, 2).repeat_interleave(g, dim=0)  # (H, ctx, D)
+        v = vf[blk, pos % bs].permute(1, 0, 2).repeat_interleave(g, dim=0)
+        rows = torch.arange(int(ql[e]))
+        mask = pos[None, :] <= (int(qo[e]) + rows)[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            qf[:, qs[e]:qs[e] + ql[e]], k, v, attn_mask=mask)
+        np.testing.assert_allclose(out[:, qs[e]:qs[e] + ql[e]], ref.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_paged_attention_golden_brute_force_and_closed_forms():
+    """Python loops over one tiny entry; a single visible key returns its V row exactly; equal
+    scores average the visible V rows."""
+    import math
+
+    q, kp, vp, table, ctx, qo, qs, ql, bs = _paged_case(2, h=2, h_kv=1, d=4, block_size=3,
+                                                         entries=((2, 2, 4),))
+    out, _ = ora.paged_attention_golden(q, kp, vp, table, ctx, qo, qs, ql, bs)
+    qf, kf, vf = (ora.bf16_bits_to_f32(a).astype(np.float64) for a in (q, kp, vp))
+    for h in range(2):
+        for m in range(2):
+            n_vis = qo[0] + m + 1
+            keys = [(table[0][n // bs], n % bs) for n in range(n_vis)]
+            s = [sum(qf[h, m, i] * kf[b, w, 0, i] for i in range(4)) / 2.0 for b, w in keys]
+            mx = max(s)
+            p = [math.exp(x - mx) for x in s]
+            o = [sum(p[j] * vf[b, w, 0, i] for j, (b, w) in enumerate(keys)) / sum(p) for i in range(4)]
+            np.testing.assert_allclose(out[h, m], o, rtol=1e-12)
+    # first query of a fresh prefill sees only position 0: o = v_0
+    q, kp, vp, table, ctx, qo, qs, ql, bs = _paged_case(3, entries=((3, 0, 3),))
+    out, _ = ora.paged_attention_golden(q, kp, vp, table, ctx, qo, qs, ql, bs)
+    v0 = ora.bf16_bits_to_f32(vp).astype(np.float64)[table[0][0], 0]
+    for h in range(out.shape[0]):
+        np.testing.assert_array_equal(out[h, 0], v0[h // 4])
+    # zero queries: uniform weights over the visible keys
+    q0 = np.zeros_like(q)
+    out, _ = ora.paged_attention_golden(q0, kp, vp, table, ctx, qo, qs, ql, bs)
+    vf = ora.bf16_bits_to_f32(vp).astype(np.float64)
+    mean2 = (vf[table[0][0], 0] + vf[table[0][0], 1]) / 2
+    np.testing.assert_allclose(out[0, 1], mean2[0], rtol=1e-12)
+
+
+def test_attention_tolerance_rejects_planted_mistakes():
+    """A dropped key, a block read from outside the entry's table and a missing scale all exceed
+    the bound; the golden itself rounded to bf16 passes. (Permuting an entry's own blocks would
+    not: a row that sees all of them is invariant to their order.)"""
+    q, kp, vp, table, ctx, qo, qs, ql, bs = _paged_case(4, d=32, entries=((6, 20, 26), (1, 40, 41)))
+    golden, cov = ora.paged_attention_golden(q, kp, vp, table, ctx, qo, qs, ql, bs)
+    vmax = float(np.abs(ora.bf16_bits_to_f32(vp)).max())
+    ok, msg = ora.attention_within_tolerance(ora.f64_to_bf16_bits(golden), golden, vmax, cov)
+    assert ok, msg
+    short = ctx.copy()
+    short[0] -= 1  # drops the last key of entry 0's last row
+    bad, _ = ora.paged_attention_golden(q, kp, vp, table, short, qo, qs, ql, bs)
+    bad[:, :5] = golden[:, :5]
+    assert not ora.attention_within_tolerance(ora.f64_to_bf16_bits(bad), golden, vmax, cov)[0]
+    foreign = table.copy()
+    spare = sorted(set(range(kp.shape[0])) - set(table[table >= 0].ravel().tolist()))
+    foreign[1, 0] = spare[0]  # a block no entry owns
+    bad, _ = ora.paged_attention_golden(q, kp, vp, foreign, ctx, qo, qs, ql, bs)
+    assert not ora.attention_within_tolerance(ora.f64_to_bf16_bits(bad), golden, vmax, cov)[0]
+    bad, _ = ora.paged_attention_golden(q, kp, vp, table, ctx, qo, qs, ql, bs, scale=1.0)
+    assert not ora.attention_within_tolerance(ora.f64_to_bf16_bits(bad), golden, vmax, cov)[0]
