@@ -729,6 +729,24 @@ def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
     int8_calls = runner.linear_calls(batch)
     int8_bytes = runner.linear_bytes(batch)
     t_int8 = time_graph(lambda: [mod(x) for mod, x in int8_calls], steps)
+    # Whole decode steps (embedding to logits), each captured in a graph at the last position:
+    # int8 and bf16 linears, each with the HIP paged attention and with the fp32 torch attention
+    # over the contiguous cache.
+    runner.enable_paged()
+    pos = context + decode_steps - 1
+    tok = inputs[-1]
+    runner.use_attention("paged")
+    paged_logits = runner.step(tok, pos).float()
+    t_step_paged = time_graph(lambda: runner.step(tok, pos), steps)
+    runner.use_attention("torch")
+    torch_logits = runner.step(tok, pos).float()
+    t_step_int8 = time_graph(lambda: runner.step(tok, pos), steps)
+    runner.use("bf16")
+    t_step_bf16 = time_graph(lambda: runner.step(tok, pos), steps)
+    runner.use_attention("paged")
+    t_step_bf16_paged = time_graph(lambda: runner.step(tok, pos), steps)
+    runner.use_attention("torch")
+    note("whole steps timed")
     h = torch.randn(batch, model.config.hidden_size, generator=gen).to(torch.bfloat16).to(dev)
     t_head = time_graph(lambda: model.lm_head(h), steps)
     head_bytes = 2 * model.lm_head.weight.numel()
@@ -740,6 +758,12 @@ def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
         "int8_linear_bytes": int8_bytes,
         "bf16_linear_us_per_step": round(t_bf16 * 1e6, 1),
         "bf16_linear_gbps": round(bf16_bytes / t_bf16 / 1e9, 1),
+        "step_us_int8_paged_attention": round(t_step_paged * 1e6, 1),
+        "step_us_int8_torch_attention": round(t_step_int8 * 1e6, 1),
+        "step_us_bf16_torch_attention": round(t_step_bf16 * 1e6, 1),
+        "step_us_bf16_paged_attention": round(t_step_bf16_paged * 1e6, 1),
+        "paged_vs_torch_attention_logit_rel_diff": round(
+            float((paged_logits - torch_logits).norm() / torch_logits.norm()), 5),
         "lm_head_bf16_us": round(t_head * 1e6, 1),
         "lm_head_gbps": round(head_bytes / t_head / 1e9, 1),
         "greedy_match_rate": round(match / (batch * decode_steps), 4),

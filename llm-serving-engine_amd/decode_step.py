@@ -22,9 +22,13 @@ applies o_proj (`attention_output`, model_runner.py:365-369).
     (x and q·s in fp32, one fp32 matmul, bf16 out; gate/up as bf16 projections, then SiLU-mul,
     as the reference's LlamaMLP rounds them) instead of the HIP kernels; it isolates the kernels
     from the quantization itself. Test and measurement use only.
-lm_head stays bf16 in both. Attention runs in fp32 over a contiguous per-layer KV cache (the
-reference's `contiguous_attention` path, model_runner.py:400-418), so both back ends see the
-same attention arithmetic and only the linears differ.
+lm_head stays bf16 in both. Attention has two implementations: "torch", fp32 over a
+contiguous per-layer KV cache (the reference's `contiguous_attention` path,
+model_runner.py:400-418), the same arithmetic for both linear back ends so only the linears
+differ; and "paged", the HIP paged attention (`ops.paged_attention_forward`, the reference's
+`attend_paged`, model_runner.py:357-363) over a per-layer pool of 16-slot blocks handed to the
+sequences in shuffled order, kept in step with the contiguous cache once `enable_paged()` has
+allocated it.
 """
 
 from __future__ import annotations
@@ -34,6 +38,7 @@ import math
 import torch
 from torch import nn
 
+from . import ops
 from .int8_linear import Int8GateUp, Int8Linear
 
 LLAMA3_8B = dict(
@@ -82,6 +87,55 @@ class DecodeRunner:
         self.v_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
         self.int8: list[dict[str, Int8Linear]] | None = None
         self.backend = "bf16"
+        self.attention = "torch"
+        self.k_pool: list[torch.Tensor] | None = None
+        self.v_pool: list[torch.Tensor] | None = None
+
+    def enable_paged(self, block_size: int = 16, seed: int = 0) -> None:
+        """Allocates a paged K/V pool per layer (the reference's allocate_kv_pool,
+        model_runner.py:107-116: (num_blocks + 1, block_size, H_KV, D), the last block a
+        scratch row) with each sequence's blocks drawn in shuffled order, and copies in what the
+        contiguous cache holds. Call before prefill, or after: both caches then stay in step."""
+        dev = self.k_cache[0].device
+        per_seq = -(-self.capacity // block_size)
+        num_blocks = self.batch * per_seq
+        g = torch.Generator().manual_seed(seed)
+        perm = torch.randperm(num_blocks, generator=g)
+        self.block_size = block_size
+        self.tables = perm.reshape(self.batch, per_seq).to(torch.int32).to(dev)
+        shape = (num_blocks + 1, block_size, self.n_kv, self.head_dim)
+        self.k_pool = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
+        self.v_pool = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
+        for i in range(len(self.layers)):
+            self._write_pool(i, self.k_cache[i], self.v_cache[i], 0, self.capacity, slice(None))
+
+    def use_attention(self, kind: str) -> None:
+        if kind not in ("torch", "paged"):
+            raise ValueError(f"unknown attention {kind!r}")
+        if kind == "paged" and self.k_pool is None:
+            raise RuntimeError("enable_paged() first")
+        self.attention = kind
+
+    def _write_pool(self, i: int, k: torch.Tensor, v: torch.Tensor, start: int, end: int,
+                    rows) -> None:
+        """k, v (nseq, H_KV, end - start, D) of sequences `rows` at positions [start, end)."""
+        pos = torch.arange(start, end, device=k.device)
+        blocks = self.tables[rows][:, pos // self.block_size].long()  # (nseq, ntok)
+        within = (pos % self.block_size).expand_as(blocks)
+        self.k_pool[i][blocks, within] = k.transpose(1, 2)
+        self.v_pool[i][blocks, within] = v.transpose(1, 2)
+
+    def _attend_paged(self, i: int, q: torch.Tensor, start: int, end: int, nseq: int,
+                      ntok: int) -> torch.Tensor:
+        """q (nseq, H, ntok, D) -> (1, nseq * ntok, H * D) through one paged attention launch."""
+        dev = q.device
+        qh = q.permute(1, 0, 2, 3).reshape(self.n_heads, nseq * ntok, self.head_dim).contiguous()
+        table = self.tables[self._rows].contiguous()
+        full = lambda v: torch.full((nseq,), v, dtype=torch.int32, device=dev)  # noqa: E731
+        q_start = torch.arange(0, nseq * ntok, ntok, dtype=torch.int32, device=dev)
+        o = ops.paged_attention_forward(qh, self.k_pool[i], self.v_pool[i], table, full(end),
+                                        full(start), q_start, full(ntok), self.block_size, ntok)
+        return o.permute(1, 0, 2).reshape(1, nseq * ntok, self.n_heads * self.head_dim)
 
     # ---- linear back ends ---------------------------------------------------------------------
 
@@ -140,10 +194,11 @@ class DecodeRunner:
 
     # ---- the step -----------------------------------------------------------------------------
 
-    def _attend(self, i: int, normed: torch.Tensor, rope, pos: torch.Tensor, nseq: int,
+    def _attend(self, i: int, normed: torch.Tensor, rope, start: int, nseq: int,
                 ntok: int) -> torch.Tensor:
-        """normed (1, nseq*ntok, hidden), sequences contiguous, positions pos (nseq, ntok) equal
-        across sequences. Writes K/V at those positions and attends causally over [0, end)."""
+        """normed (1, nseq*ntok, hidden), sequences contiguous, every sequence at positions
+        [start, start + ntok). Writes K/V there and attends causally over [0, end). The
+        positions come in as a host int, so a step captures into a graph."""
         from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
         q, k, v = self._qkv(i, normed)
@@ -152,10 +207,13 @@ class DecodeRunner:
         v = v.reshape(nseq, ntok, self.n_kv, self.head_dim).transpose(1, 2)
         cos, sin = rope
         q, k = apply_rotary_pos_emb(q, k, cos, sin)
-        start = int(pos[0, 0])
         end = start + ntok
         self.k_cache[i][self._rows, :, start:end] = k
         self.v_cache[i][self._rows, :, start:end] = v
+        if self.k_pool is not None:
+            self._write_pool(i, k, v, start, end, self._rows)
+        if self.attention == "paged":
+            return self._o(i, self._attend_paged(i, q, start, end, nseq, ntok))
         keys = self.k_cache[i][self._rows, :, :end].float()
         vals = self.v_cache[i][self._rows, :, :end].float()
         rep = self.n_heads // self.n_kv
@@ -183,7 +241,8 @@ class DecodeRunner:
         cos, sin = model.rotary_emb(hidden, pos.reshape(1, -1))
         rope = (cos.reshape(nseq, ntok, -1), sin.reshape(nseq, ntok, -1))
         for i, layer in enumerate(self.layers):
-            hidden = hidden + self._attend(i, layer.input_layernorm(hidden), rope, pos, nseq, ntok)
+            hidden = hidden + self._attend(i, layer.input_layernorm(hidden), rope, start, nseq,
+                                           ntok)
             hidden = hidden + self._mlp(i, layer.post_attention_layernorm(hidden))
         return model.norm(hidden)
 

@@ -74,3 +74,24 @@ def test_int8_linear_stack_replays_from_a_graph(runner, dev):
         torch.cuda.synchronize()
         for a, b in zip(eager, outs):
             assert torch.equal(a, b)
+
+
+def test_paged_attention_matches_the_torch_attention(runner, dev):
+    """One int8 decode step through the HIP paged attention (shuffled 16-slot blocks) and through
+    the fp32 torch attention over the contiguous cache: logits agree to the bf16 rounding of the
+    probabilities, and so do the greedy tokens."""
+    if runner.int8 is None:
+        runner.quantize("int8")
+    runner.use("int8")
+    if runner.k_pool is None:
+        runner.enable_paged()
+    gen = torch.Generator().manual_seed(15)
+    tok = torch.randint(0, runner.model.config.vocab_size, (16,), generator=gen).to(dev)
+    runner.use_attention("torch")
+    ref = runner.step(tok, 36).float()
+    runner.use_attention("paged")
+    got = runner.step(tok, 36).float()
+    runner.use_attention("torch")
+    rel = (got - ref).norm() / ref.norm()
+    assert rel < 1e-2, f"relative logit difference {rel:.4f}"
+    assert int((got.argmax(-1) == ref.argmax(-1)).sum()) >= 15
