@@ -237,6 +237,29 @@ def bench_w8a8(pkg, dev, steps: int, gen) -> dict:
 
         t = time_region(step, max(2, steps // 4), 1) / max(2, steps // 4)
         res[str(m)] = {"tops": round(ops / t / 1e12, 2), "ms": round(t * 1e3, 3)}
+    res["rmsnorm_quantize"] = bench_rmsnorm_quantize(pkg, dev, steps, gen)
+    return res
+
+
+def bench_rmsnorm_quantize(pkg, dev, steps: int, gen) -> dict:
+    """The decoder norm fused with per-token quantization (hidden 4096) against transformers'
+    LlamaRMSNorm followed by the separate quantizer: us per call, and GB/s of algorithmic bytes
+    (x in, weight, xq and sx out)."""
+    import torch
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+
+    k = 4096
+    norm = LlamaRMSNorm(k, eps=1e-5).to(device=dev, dtype=torch.bfloat16)
+    res = {}
+    for m in (64, 2048):
+        x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+        fused = lambda x=x: pkg.ops.rmsnorm_quantize(x, norm.weight, 1e-5)  # noqa: E731
+        unfused = lambda x=x: pkg.ops.quantize_act_per_token(norm(x))  # noqa: E731
+        t = time_region(fused, steps, 2) / steps
+        t0 = time_region(unfused, steps, 2) / steps
+        nbytes = 2 * m * k + 2 * k + m * k + 4 * m
+        res[str(m)] = {"fused_us": round(t * 1e6, 2), "fused_gbps": round(nbytes / t / 1e9, 1),
+                       "unfused_us": round(t0 * 1e6, 2)}
     return res
 
 

@@ -76,7 +76,7 @@ enum lse_query_key {
   LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
 };
 
-#define LSE_ABI_VERSION 5
+#define LSE_ABI_VERSION 6
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -143,6 +143,23 @@ int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const floa
  */
 int lse_quantize_act_per_token(const void* x, int64_t ldx, int8_t* xq, float* sx,
                                int64_t M, int64_t K, void* stream);
+
+/*
+ * RMSNorm followed by per-token quantization, in one pass over each token row (the W8A8 first
+ * stage fused into the decoder's norms). With the rounding steps of LlamaRMSNorm:
+ *   r = 1 / sqrt(fl32(sum_k x[m,k]^2 / K) + eps),  h[m,k] = bf16(weight[k] * bf16(x[m,k] * r))
+ * then sx[m] and xq[m,k] from h exactly as lse_quantize_act_per_token computes them from a bf16
+ * row. The sum of squares runs in a fixed fp32 order (tree over the row), so h can differ from
+ * another implementation's in the last bf16 place where x * r lies at a rounding boundary.
+ * x: (M, K) bf16, row stride ldx (multiple of 8, 16-byte aligned). weight: (K) bf16, 16-byte
+ * aligned. xq: (M, K) int8 contiguous. sx: (M) fp32. normed: (M, K) bf16 contiguous receiving h,
+ * or NULL. K % LSE_K_ALIGN == 0.
+ * Replaces: `input_layernorm` / `post_attention_layernorm` (LlamaRMSNorm.forward,
+ * modeling_llama.py:62-67) at model_runner.py:222-223, followed by the activation quantization
+ * of the W8A8 mode.
+ */
+int lse_rmsnorm_quantize(const void* x, int64_t ldx, const void* weight, float eps, int8_t* xq,
+                         float* sx, void* normed, int64_t M, int64_t K, void* stream);
 
 /*
  * W8A8 linear: acc[m,n] = sum_k xq[m,k] * q[n,k] exactly in int32;

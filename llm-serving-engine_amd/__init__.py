@@ -6,8 +6,16 @@ it as `llm_serving_engine_amd`.
 
 from . import ops
 from ._lib import LIB_PATH, library
+from .checkpoint import load_int8_checkpoint, save_int8_checkpoint
 from .config import ModelConfig
-from .int8_linear import Int8GateUp, Int8GluMLP, Int8Linear, check_linear_supported
+from .int8_linear import (
+    Int8GateUp,
+    Int8GluMLP,
+    Int8Linear,
+    Int8RMSNormQuant,
+    QuantizedRows,
+    check_linear_supported,
+)
 from .quantize import check_int8_support, quantize_model_
 
 __all__ = [
@@ -15,10 +23,14 @@ __all__ = [
     "Int8GateUp",
     "Int8GluMLP",
     "Int8Linear",
+    "Int8RMSNormQuant",
     "ModelConfig",
+    "QuantizedRows",
     "check_int8_support",
     "check_linear_supported",
     "library",
+    "load_int8_checkpoint",
     "ops",
     "quantize_model_",
+    "save_int8_checkpoint",
 ]

@@ -12,6 +12,9 @@ int launch_quantize_weight(const float* w, int64_t ldw, int8_t* q, float* s, int
                            hipStream_t stream);
 int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, int64_t M,
                         int64_t K, hipStream_t stream);
+int launch_rmsnorm_quantize(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
+                            int8_t* xq, float* sx, uint16_t* normed, int64_t M, int64_t K,
+                            hipStream_t stream);
 int launch_pack_weight(const int8_t* q, int64_t N, int64_t K, int8_t* qp, hipStream_t stream);
 int launch_pack_glu(const int8_t* q, int64_t I, int64_t K, int8_t* qp, hipStream_t stream);
 int64_t packed_weight_bytes(int64_t N, int64_t K);
@@ -163,6 +166,20 @@ int lse_quantize_act_per_token(const void* x, int64_t ldx, int8_t* xq, float* sx
   if (int st = check_bf16_matrix(x, ldx, M, K, 8)) return st;
   if (K > 0 && !aligned(xq, 16)) return LSE_E_ALIGN;
   return lse::launch_quantize_act((const uint16_t*)x, ldx, xq, sx, M, K, (hipStream_t)stream);
+}
+
+int lse_rmsnorm_quantize(const void* x, int64_t ldx, const void* weight, float eps, int8_t* xq,
+                         float* sx, void* normed, int64_t M, int64_t K, void* stream) {
+  if (M < 0 || K < 0 || M > kMaxGridX) return LSE_E_SHAPE;
+  if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
+  if (M == 0 || K == 0) return LSE_OK;
+  if (!weight || !xq || !sx) return LSE_E_NULL;
+  if (int st = check_bf16_matrix(x, ldx, M, K, 8)) return st;
+  if (!aligned(weight, 16) || !aligned(xq, 16) || (normed && !aligned(normed, 16)))
+    return LSE_E_ALIGN;
+  if (!(eps >= 0.0f)) return LSE_E_SHAPE;
+  return lse::launch_rmsnorm_quantize((const uint16_t*)x, ldx, (const uint16_t*)weight, eps, xq,
+                                      sx, (uint16_t*)normed, M, K, (hipStream_t)stream);
 }
 
 int64_t lse_packed_weight_bytes(int64_t N, int64_t K) {

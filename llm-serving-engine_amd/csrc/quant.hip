@@ -88,6 +88,97 @@ quantize_act_rows(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restric
   }
 }
 
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();  // red may still be read by an earlier reduction
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < kQuantThreads / 64; ++w) t += red[w];
+  return t;
+}
+
+// RMSNorm of one token row followed by its per-token quantization (W8A8 first stage fused into
+// the decoder's input_layernorm / post_attention_layernorm). With the rounding steps of
+// transformers' LlamaRMSNorm (modeling_llama.py:62-67: fp32 variance, x * rsqrt(var + eps)
+// rounded to bf16, times the bf16 weight rounded to bf16):
+//   r = 1 / sqrt(fl32(sum_k x^2 / K) + eps),  h_k = bf16(w_k * bf16(x_k * r))
+// then sx = fl32(amax_k |h_k| / 127) and xq_k = clamp(rne(h_k / sx), -127, 127), exactly as
+// quantize_act_rows does for an existing bf16 row. One workgroup per token; the row is read three
+// times (sum of squares, amax, quantize), the last two from L2. `normed` (optional) receives h.
+__device__ __forceinline__ float rms_h(uint32_t xb, uint32_t wb, float r) {
+  const float x = __builtin_bit_cast(float, xb);
+  const float h = bf16_to_f32(f32_to_bf16(x * r));
+  return bf16_to_f32(f32_to_bf16(__builtin_bit_cast(float, wb) * h));
+}
+
+__global__ void __launch_bounds__(kQuantThreads)
+rmsnorm_quant_rows(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
+                   float eps, int8_t* __restrict__ xq, float* __restrict__ sx,
+                   uint16_t* __restrict__ normed, int K) {
+  __shared__ float red[kQuantThreads / 64];
+  const int64_t m = blockIdx.x;
+  const uint16_t* row = x + m * ldx;
+  float ss = 0.0f;
+  for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + k);
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = __builtin_bit_cast(float, u[i] << 16);
+      const float b = __builtin_bit_cast(float, u[i] & 0xffff0000u);
+      ss = __builtin_fmaf(a, a, ss);
+      ss = __builtin_fmaf(b, b, ss);
+    }
+  }
+  const float var = block_sum(ss, red) / (float)K;
+  const float r = 1.0f / __builtin_sqrtf(var + eps);
+  float amax = 0.0f;
+  for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + k);
+    const uint4 g = *reinterpret_cast<const uint4*>(w + k);
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w}, gw[4] = {g.x, g.y, g.z, g.w};
+    uint32_t hb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = rms_h(u[i] << 16, gw[i] << 16, r);
+      const float hi = rms_h(u[i] & 0xffff0000u, gw[i] & 0xffff0000u, r);
+      amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
+      hb[i] = pack_bf16x2(lo, hi);
+    }
+    if (normed) *reinterpret_cast<uint4*>(normed + m * K + k) = make_uint4(hb[0], hb[1], hb[2], hb[3]);
+  }
+  __syncthreads();  // the sum's reads of red are done before block_max writes it
+  const float scale = row_scale(block_max(amax, red));
+  if (threadIdx.x == 0) sx[m] = scale;
+  int8_t* out = xq + m * K;
+  for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + k);
+    const uint4 g = *reinterpret_cast<const uint4*>(w + k);
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w}, gw[4] = {g.x, g.y, g.z, g.w};
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (uint8_t)quant1(rms_h(u[i] << 16, gw[i] << 16, r), scale);
+      const uint32_t hi =
+          (uint8_t)quant1(rms_h(u[i] & 0xffff0000u, gw[i] & 0xffff0000u, r), scale);
+      packed[i >> 1] |= (lo | (hi << 8)) << (16 * (i & 1));
+    }
+    *reinterpret_cast<uint2*>(out + k) = make_uint2(packed[0], packed[1]);
+  }
+}
+
+int launch_rmsnorm_quantize(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
+                            int8_t* xq, float* sx, uint16_t* normed, int64_t M, int64_t K,
+                            hipStream_t stream) {
+  hipLaunchKernelGGL(rmsnorm_quant_rows, dim3((unsigned)M), dim3(kQuantThreads), 0, stream, x, ldx,
+                     w, eps, xq, sx, normed, (int)K);
+  return launch_status();
+}
+
 int launch_quantize_weight(const float* w, int64_t ldw, int8_t* q, float* s, int64_t N, int64_t K,
                            hipStream_t stream) {
   hipLaunchKernelGGL(quantize_weight_rows, dim3((unsigned)N), dim3(kQuantThreads), 0, stream, w,

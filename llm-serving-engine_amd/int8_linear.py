@@ -26,6 +26,29 @@ from . import _lib, ops
 MODES = ("int8", "w8a8")
 
 
+class QuantizedRows:
+    """The W8A8 form of a bf16 activation (..., K): int8 rows `xq` (rows, K) and per-row fp32
+    scales `sx`, as `Int8RMSNormQuant` produces them. It stands where the norm's bf16 output
+    stood: W8A8 projections take it as their input without quantizing again, and it answers the
+    `shape`, `device` and `dtype` (that of the activation it encodes) the callers read
+    (model_runner.py:319, 383-386; modeling_llama.py:251)."""
+
+    __slots__ = ("xq", "sx", "shape", "device", "dtype")
+
+    def __init__(self, xq: torch.Tensor, sx: torch.Tensor, shape: torch.Size,
+                 dtype: torch.dtype = torch.bfloat16) -> None:
+        self.xq, self.sx, self.shape = xq, sx, torch.Size(shape)
+        self.device, self.dtype = xq.device, dtype
+
+
+def _w8a8_input(mod: nn.Module, x) -> bool:
+    if isinstance(x, QuantizedRows):
+        if mod.mode != "w8a8":
+            raise RuntimeError("pre-quantized rows reach a weight-only (int8) projection")
+        return True
+    return False
+
+
 class Int8Linear(nn.Module):
     """y = x · (q · diag(s))ᵀ (+ bias). `mode` "int8" is weight-only W8A16 (the reference's own
     name for the switch, model_runner.py:46); "w8a8" adds dynamic per-token activation
@@ -87,8 +110,11 @@ class Int8Linear(nn.Module):
         """The int8 weight as a row-major (N, K) matrix."""
         return ops.unpack_weight(self.qweight, self.out_features, self.in_features)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.mode == "int8":
+    def forward(self, x: torch.Tensor | QuantizedRows) -> torch.Tensor:
+        if _w8a8_input(self, x):
+            y, _ = ops.w8a8_gemm(x.xq, x.sx, self.qweight, self.scales)
+            y = y.view(*x.shape[:-1], self.out_features)
+        elif self.mode == "int8":
             y = ops.w8a16_linear(x, self.qweight, self.scales)
         else:
             y = ops.w8a8_linear(x, self.qweight, self.scales)
@@ -180,7 +206,10 @@ class Int8GateUp(nn.Module):
         """The stacked (2I, K) int8 [gate; up] weight, row-major."""
         return ops.unpack_glu(self.qweight, self.intermediate_size, self.in_features)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor | QuantizedRows) -> torch.Tensor:
+        if _w8a8_input(self, x):
+            h = ops.w8a8_glu_quantized(x.xq, x.sx, self.qweight, self.scales)
+            return h.view(*x.shape[:-1], self.intermediate_size)
         if self.mode == "int8":
             return ops.w8a16_glu(x, self.qweight, self.scales)
         return ops.w8a8_glu(x, self.qweight, self.scales)
@@ -217,3 +246,22 @@ def fusable_mlp(mlp: nn.Module) -> bool:
     return (all(isinstance(p, nn.Linear) for p in parts)
             and _is_silu(getattr(mlp, "act_fn", None))
             and parts[0].bias is None and parts[1].bias is None)
+
+
+class Int8RMSNormQuant(nn.Module):
+    """Drop-in for a decoder layer's `input_layernorm` / `post_attention_layernorm` (LlamaRMSNorm,
+    modeling_llama.py:53-67) in the W8A8 mode: the norm and the per-token quantization its W8A8
+    consumers would each repeat run as one kernel, and the result travels as `QuantizedRows`.
+    The bf16 weight stays a Parameter (the runner reads `model.dtype` off the first one)."""
+
+    def __init__(self, norm: nn.Module) -> None:
+        super().__init__()
+        self.weight = norm.weight
+        self.variance_epsilon = norm.variance_epsilon
+
+    def forward(self, x: torch.Tensor) -> QuantizedRows:
+        xq, sx, _ = ops.rmsnorm_quantize(x, self.weight, self.variance_epsilon)
+        return QuantizedRows(xq, sx, x.shape, x.dtype)
+
+    def extra_repr(self) -> str:
+        return f"{tuple(self.weight.shape)}, eps={self.variance_epsilon}, quantize=per-token int8"

@@ -24,10 +24,12 @@ __all__ = [
     "packed_shape",
     "quantize_act_per_token",
     "quantize_weight_per_channel",
+    "rmsnorm_quantize",
     "unpack_glu",
     "unpack_weight",
     "w8a8_gemm",
     "w8a8_glu",
+    "w8a8_glu_quantized",
     "w8a8_linear",
     "w8a16_glu",
     "w8a16_linear",
@@ -285,10 +287,20 @@ def w8a16_glu(
 def w8a8_glu(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     """Dynamic per-token W8A8 form of `w8a16_glu`: x quantized per row, exact int32 sums,
     g = (acc_g * sx) * s_g, u likewise, h = bf16(silu(g) * u). x (..., K) → h (..., I)."""
-    dev = _on_gpu(x, qp, scales)
-    i = _glu_scales(scales)
     xq, sx = quantize_act_per_token(x)
+    h = w8a8_glu_quantized(xq, sx, qp, scales)
+    return h.view(*x.shape[:-1], h.shape[-1])
+
+
+def w8a8_glu_quantized(xq: torch.Tensor, sx: torch.Tensor, qp: torch.Tensor,
+                       scales: torch.Tensor) -> torch.Tensor:
+    """`w8a8_glu` from already quantized rows: xq (M, K) int8, sx (M,) fp32 → h (M, I) bf16."""
+    dev = _on_gpu(xq, sx, qp, scales)
+    i = _glu_scales(scales)
+    _require(xq.dim() == 2 and xq.dtype == torch.int8 and xq.is_contiguous(),
+             "xq must be contiguous (M, K) int8")
     m, k = xq.shape
+    _require(sx.dtype == torch.float32 and sx.shape == (m,), "sx must be fp32 (M,)")
     _check_packed(qp, i, k, glu=True)
     h = torch.empty((m, i), dtype=torch.bfloat16, device=dev)
     _lib.check(
@@ -298,7 +310,7 @@ def w8a8_glu(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor) -> torch.T
         ),
         "lse_w8a8_glu",
     )
-    return h.view(*x.shape[:-1], i)
+    return h
 
 
 def paged_attention_forward(
@@ -352,3 +364,31 @@ def paged_attention_forward(
         "lse_paged_attention",
     )
     return o
+
+
+def rmsnorm_quantize(
+    x: torch.Tensor, weight: torch.Tensor, eps: float, want_normed: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """LlamaRMSNorm (transformers modeling_llama.py:62-67) and per-token int8 quantization of its
+    bf16 output in one kernel: x (..., K) bf16, weight (K,) bf16 → (xq (rows, K) int8, sx (rows,)
+    fp32, normed (rows, K) bf16 or None)."""
+    dev = _on_gpu(x, weight)
+    _require(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16,
+             f"RMSNorm-quantize takes bf16 x and weight, got {x.dtype}, {weight.dtype}")
+    k = x.shape[-1]
+    _require(weight.shape == (k,), f"weight must be ({k},), got {tuple(weight.shape)}")
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    w = weight.contiguous()
+    xq = torch.empty((m, k), dtype=torch.int8, device=dev)
+    sx = torch.empty((m,), dtype=torch.float32, device=dev)
+    normed = torch.empty((m, k), dtype=torch.bfloat16, device=dev) if want_normed else None
+    _lib.check(
+        _lib.library().lse_rmsnorm_quantize(
+            x2.data_ptr(), x2.stride(0) if m > 1 else k, w.data_ptr(), float(eps),
+            xq.data_ptr(), sx.data_ptr(), normed.data_ptr() if normed is not None else None, m,
+            k, _stream(dev),
+        ),
+        "lse_rmsnorm_quantize",
+    )
+    return xq, sx, normed

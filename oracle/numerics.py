@@ -286,3 +286,20 @@ def attention_within_tolerance(o_bits: np.ndarray, golden: np.ndarray, v_absmax:
     bound = 2.0 ** -8 * (v_absmax + np.abs(g))
     worst = float(np.max(err / bound))
     return worst <= 1.0, f"max err {float(err.max()):.3e}, worst err/bound {worst:.3f}"
+
+
+# ---- RMSNorm fused with per-token quantization ----------------------------------------------
+
+
+def rmsnorm_bf16(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
+    """LlamaRMSNorm's roundings (transformers modeling_llama.py:62-67) on bf16 rows (M, K):
+    var = fl32(mean x^2) (the mean in fp64, rounded once), r = fl32(1 / fl32(sqrt(var + eps))),
+    h = bf16(w * bf16(fl32(x * r))). Returns h as bf16 bits. Implementations that sum the
+    squares in another fp32 order can differ in the last bf16 place where x * r lies at a
+    rounding boundary."""
+    x = bf16_bits_to_f32(x_bits)
+    var = np.mean(x.astype(np.float64) ** 2, axis=1).astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt((var + np.float32(eps)).astype(np.float32))).astype(np.float32)
+    h = bf16_bits_to_f32(f32_to_bf16_bits((x * r[:, None]).astype(np.float32)))
+    w = bf16_bits_to_f32(np.asarray(w_bits, np.uint16))
+    return f32_to_bf16_bits((w[None, :] * h).astype(np.float32))

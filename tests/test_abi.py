@@ -190,3 +190,15 @@ def test_glu_entry_points_reject_bad_arguments(pkg):
     assert lib.lse_w8a8_glu(ctypes.c_void_p((1 << 20) + 4), FAKE, FAKE, FAKE, FAKE, 64, 2, 64,
                             64, None) == E_ALIGN
     assert lib.lse_w8a8_glu(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 2, 64, 64, None) == E_SHAPE
+
+
+def test_rmsnorm_quantize_rejects_bad_arguments(pkg):
+    lib = pkg.library()
+    # (x, ldx, weight, eps, xq, sx, normed, M, K)
+    assert lib.lse_rmsnorm_quantize(FAKE, 64, FAKE, 1e-5, FAKE, FAKE, None, 2, 40, None) == E_ALIGN
+    assert lib.lse_rmsnorm_quantize(FAKE, 64, None, 1e-5, FAKE, FAKE, None, 2, 64, None) == E_NULL
+    assert lib.lse_rmsnorm_quantize(FAKE, 32, FAKE, 1e-5, FAKE, FAKE, None, 2, 64, None) == E_SHAPE
+    assert lib.lse_rmsnorm_quantize(FAKE, 64, FAKE, -1.0, FAKE, FAKE, None, 2, 64, None) == E_SHAPE
+    assert lib.lse_rmsnorm_quantize(FAKE, 64, ctypes.c_void_p((1 << 20) + 2), 1e-5, FAKE, FAKE,
+                                    None, 2, 64, None) == E_ALIGN
+    assert lib.lse_rmsnorm_quantize(None, 64, None, 1e-5, None, None, None, 0, 64, None) == 0

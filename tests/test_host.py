@@ -127,3 +127,62 @@ def test_mlp_fusion_eligibility(pkg):
     assert not fusable_mlp(LlamaMLP(LlamaConfig(hidden_size=32, intermediate_size=64,
                                                 mlp_bias=True)))
     assert not fusable_mlp(nn.Linear(4, 4))
+
+
+def _cpu_int8_llama(pkg, fused: bool):
+    """A tiny Llama whose projections are CPU int8 modules (zeros; no kernel calls)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=32, hidden_size=32, intermediate_size=64, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2)
+    model = LlamaForCausalLM(cfg).to(torch.bfloat16)
+    for layer in model.model.layers:
+        a = layer.self_attn
+        for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            lin = getattr(a, name)
+            setattr(a, name, pkg.Int8Linear(lin.in_features, lin.out_features, "int8", device="cpu"))
+        if fused:
+            layer.mlp = pkg.Int8GluMLP(pkg.Int8GateUp(32, 64, "int8", device="cpu"),
+                                       pkg.Int8Linear(64, 32, "int8", device="cpu"))
+        else:
+            for name, (k, n) in (("gate_proj", (32, 64)), ("up_proj", (32, 64)),
+                                 ("down_proj", (64, 32))):
+                setattr(layer.mlp, name, pkg.Int8Linear(k, n, "int8", device="cpu"))
+    return model
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_checkpoint_layout(pkg, tmp_path, fused):
+    """Tensor names, dtypes and shapes of the int8 checkpoint format, and its metadata."""
+    import json
+
+    from safetensors import safe_open
+
+    from llm_serving_engine_amd import checkpoint
+
+    path = pkg.save_int8_checkpoint(_cpu_int8_llama(pkg, fused), tmp_path / "m.safetensors")
+    meta = checkpoint.read_metadata(path)
+    assert meta["mode"] == "int8" and json.loads(meta["config"])["hidden_size"] == 32
+    with safe_open(str(path), "pt") as f:
+        keys = set(f.keys())
+        q = f.get_tensor("model.layers.1.mlp.up_proj.qweight")
+        assert q.dtype == torch.int8 and tuple(q.shape) == (64, 32)
+        s = f.get_tensor("model.layers.0.self_attn.k_proj.scales")
+        assert s.dtype == torch.float32 and tuple(s.shape) == (16,)
+        assert f.get_tensor("model.norm.weight").dtype == torch.bfloat16
+    assert "lm_head.weight" in keys and "model.embed_tokens.weight" in keys
+    assert not any(k.endswith("proj.weight") or ".gate_up." in k for k in keys)
+
+
+def test_checkpoint_reader_refuses_other_files(pkg, tmp_path):
+    from safetensors.torch import save_file
+
+    from llm_serving_engine_amd import checkpoint
+
+    save_file({"x": torch.zeros(2)}, str(tmp_path / "plain.safetensors"))
+    with pytest.raises(RuntimeError, match="not an lse-int8 checkpoint"):
+        checkpoint.read_metadata(tmp_path / "plain.safetensors")
+    save_file({"x": torch.zeros(2)}, str(tmp_path / "v9.safetensors"),
+              metadata={"format": "lse-int8", "format_version": "9"})
+    with pytest.raises(RuntimeError, match="format_version"):
+        checkpoint.read_metadata(tmp_path / "v9.safetensors")

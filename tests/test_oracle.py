@@ -496,3 +496,36 @@ def test_attention_tolerance_rejects_planted_mistakes():
     assert not ora.attention_within_tolerance(ora.f64_to_bf16_bits(bad), golden, vmax, cov)[0]
     bad, _ = ora.paged_attention_golden(q, kp, vp, table, ctx, qo, qs, ql, bs, scale=1.0)
     assert not ora.attention_within_tolerance(ora.f64_to_bf16_bits(bad), golden, vmax, cov)[0]
+
+
+# ---- RMSNorm ---------------------------------------------------------------------------------
+
+
+def test_rmsnorm_matches_llama_rmsnorm():
+    """Against transformers' LlamaRMSNorm itself on bf16 rows (CPU): equal bits except where the
+    two fp32 variance sums put x * r on opposite sides of a bf16 rounding boundary; that 1-ulp
+    difference of the inner rounding, carried through the product with the weight and its own
+    rounding, moves the output by at most 2 ulps, and rarely."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+
+    rng = np.random.default_rng(11)
+    m, k = 64, 4096
+    x = rng.standard_normal((m, k), dtype=np.float32) * np.float32(3.0)
+    x[3] = 0.0  # an all-zero row: r = 1/sqrt(eps), h = 0
+    x_bits = ora.f32_to_bf16_bits(x)
+    w_bits = ora.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(k, dtype=np.float32))
+    norm = LlamaRMSNorm(k, eps=1e-5).to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(torch.from_numpy(w_bits.view(np.int16)).view(torch.bfloat16))
+        ref = norm(torch.from_numpy(x_bits.view(np.int16)).view(torch.bfloat16))
+    ref_bits = ref.view(torch.int16).numpy().view(np.uint16)
+    ours = ora.rmsnorm_bf16(x_bits, w_bits, 1e-5)
+    diff = ora.bf16_ulps_apart(ours, ora.bf16_bits_to_f32(ref_bits).astype(np.float64))
+    assert diff.max() <= 2.0 and np.mean(diff > 0) < 1e-3, (diff.max(), np.mean(diff > 0))
+    assert np.all(ours[3] == 0)
+    # eps placement: rows of one repeated value v give h = w * v / sqrt(v^2 + eps)
+    v = np.full((1, k), 0.001, np.float32)
+    h = ora.bf16_bits_to_f32(ora.rmsnorm_bf16(ora.f32_to_bf16_bits(v), ora.f32_to_bf16_bits(
+        np.ones(k, np.float32)), 1e-5))
+    vb = float(ora.bf16_bits_to_f32(ora.f32_to_bf16_bits(v))[0, 0])
+    np.testing.assert_allclose(h[0, 0], vb / np.sqrt(vb * vb + 1e-5), rtol=2 ** -7)
