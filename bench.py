@@ -69,7 +69,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true", help="skip prefill and W8A8 figures")
     p.add_argument("--only", choices=["decode", "prefill", "w8a8", "glu", "attention",
-                                      "decode-step"],
+                                      "lm-head", "decode-step"],
                    help="one family; decode-step is config 4 (a 32-layer model's decode step)")
     p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
                    help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
@@ -312,6 +312,30 @@ def bench_glu(pkg, dev, steps: int, gen) -> dict:
     res["prefill_M2048"] = {"us": round(t * 1e6, 1), "tflops": round(4 * m * i * k / t / 1e12, 1),
                             "mfma_frac": round(4 * m * i * k / t / 1e12 / BF16_PEAK_TFLOPS, 4),
                             "unfused_us": round(t0 * 1e6, 1)}
+    return res
+
+
+def bench_lm_head(pkg, dev, steps: int, gen) -> dict:
+    """The bf16 lm_head of Llama-3 (N = 128256, K = 4096, 1.05 GB) at decode batch sizes: the
+    decode kernel on the bf16 tile layout against torch's F.linear (the vendor BLAS, the
+    reference's own call), us and GB/s (2NK + 2MK + 2MN bytes), over 2 weight copies so every
+    call streams its weight from HBM."""
+    import torch
+
+    n, k = 128256, 4096
+    ws = [(torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(dev) for _ in range(2)]
+    wps = [pkg.ops.pack_bf16_weight(w) for w in ws]
+    res = {}
+    for m in DECODE_MS:
+        x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+        ours = lambda x=x: [pkg.ops.bf16_decode_linear(x, wp, n) for wp in wps]  # noqa: E731
+        blas = lambda x=x: [torch.nn.functional.linear(x, w) for w in ws]  # noqa: E731
+        t = time_graph(ours, steps) / 2
+        t0 = time_graph(blas, steps) / 2
+        nbytes = 2 * n * k + 2 * m * k + 2 * m * n
+        res[str(m)] = {"us": round(t * 1e6, 1), "gbps": round(nbytes / t / 1e9, 1),
+                       "vendor_blas_us": round(t0 * 1e6, 1),
+                       "vendor_blas_gbps": round(nbytes / t0 / 1e9, 1)}
     return res
 
 
@@ -839,6 +863,9 @@ def main() -> None:
         return
     if args.only == "glu":
         print(json.dumps({"fused_gate_up": bench_glu(pkg, dev, args.steps, gen)}))
+        return
+    if args.only == "lm-head":
+        print(json.dumps({"lm_head_bf16": bench_lm_head(pkg, dev, args.steps, gen)}))
         return
     if args.only == "attention":
         print(json.dumps({"paged_attention": bench_attention(pkg, dev, args.steps, gen)}))

@@ -76,7 +76,7 @@ enum lse_query_key {
   LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
 };
 
-#define LSE_ABI_VERSION 6
+#define LSE_ABI_VERSION 7
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -256,6 +256,32 @@ int lse_paged_attention(const void* q, int64_t q_stride_h, int64_t q_stride_t,
                         int64_t H_KV, int64_t D, int64_t block_size, int64_t max_blocks,
                         int64_t max_q_len, float softmax_scale, void* workspace,
                         int64_t workspace_bytes, void* stream);
+
+/* Bytes of the bf16 tile layout of an (N, K) weight: ceil(N/16) * ceil(K/64) * 2048. */
+int64_t lse_packed_bf16_weight_bytes(int64_t N, int64_t K);
+
+/*
+ * Packs a row-major (N, K) bf16 weight (row stride ldw, a multiple of 8, 16-byte aligned;
+ * K % LSE_K_ALIGN == 0) into the bf16 tile layout lse_bf16_decode_gemm reads: 16 rows x 64 K
+ * per step, 2 KB, byte (rb * ceil(K/64) + j) * 2048 + 1024 h + 16 l + 2 i holding
+ * w[16 rb + l % 16][64 j + 16 (l / 16) + 8 h + i], zero past N and K. Load time only.
+ * Replaces: the row-major bf16 `lm_head.weight` (its storage step; the reference computes
+ * `get_output_embeddings()(hidden)` at model_runner.py:306-307).
+ */
+int lse_pack_bf16_weight(const void* w, int64_t ldw, int64_t N, int64_t K, void* wp,
+                         void* stream);
+
+/*
+ * bf16 linear for decode-sized batches (the lm_head the int8 path keeps in bf16):
+ *   y[m,n] = bf16_rne(sum_k x[m,k] * w[n,k]), fp32 accumulation, M <= LSE_DECODE_MAX_M.
+ * x: (M, K) bf16, row stride ldx (multiple of 8, 16-byte aligned). wp: lse_pack_bf16_weight
+ * layout. y: (M, N) bf16, row stride ldy >= N. Deterministic as the int8 decode GEMMs are.
+ * Returns LSE_E_ALGO for M > LSE_DECODE_MAX_M.
+ * Replaces: `F.linear(hidden, lm_head.weight)` in `emit_owed` (model_runner.py:306-307) and the
+ * graphed decode step (decode_graph.py:140).
+ */
+int lse_bf16_decode_gemm(const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy,
+                         int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Static properties (enum lse_query_key); -1 for an unknown key. Load-time checks read these,
  * as `ModelRunner.check_custom_kernel_support` (model_runner.py:77-94) checks its kernels. */

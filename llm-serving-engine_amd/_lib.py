@@ -32,6 +32,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lse_pack_glu": (_INT, [_P, _I64, _I64, _P, _P]),
     "lse_w8a16_glu": (_INT, [_P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]),
     "lse_w8a8_glu": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "lse_packed_bf16_weight_bytes": (_I64, [_I64, _I64]),
+    "lse_pack_bf16_weight": (_INT, [_P, _I64, _I64, _I64, _P, _P]),
+    "lse_bf16_decode_gemm": (_INT, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "lse_paged_attention_workspace_bytes": (_I64, [_I64] * 7),
     "lse_paged_attention": (_INT, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P,
                                    _P, _P, _I64, _I64] + [_I64] * 7 + [ctypes.c_float, _P, _I64,
@@ -46,7 +49,7 @@ ALGO_AUTO, ALGO_DECODE, ALGO_PREFILL = 0, 1, 2
 MODE_W8A16, MODE_W8A8 = 0, 1
 E_WORKSPACE = -6
 Q_ABI_VERSION, Q_K_ALIGN, Q_DECODE_MAX_M, Q_MAX_K, Q_GFX_ARCH = 0, 1, 2, 3, 4
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -43,6 +43,11 @@ int launch_w8a16_gemm_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, cons
 int launch_w8a8_gemm_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
                          uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
                          hipStream_t stream);
+int64_t packed_bf16_bytes(int64_t N, int64_t K);
+int launch_pack_bf16(const uint16_t* w, int64_t ldw, int64_t N, int64_t K, uint16_t* wp,
+                     hipStream_t stream);
+int launch_bf16_skinny(const uint16_t* x, int64_t ldx, const uint16_t* wp, uint16_t* y,
+                       int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 int64_t paged_attention_workspace_bytes(int64_t entries, int64_t H, int64_t HKV, int64_t D,
                                         int64_t max_q_len, int64_t max_ctx);
 int launch_paged_attention(const uint16_t* q, int64_t sq_h, int64_t sq_t, const uint16_t* k_pool,
@@ -389,6 +394,41 @@ int lse_paged_attention(const void* q, int64_t q_stride_h, int64_t q_stride_t,
       block_table_stride, context_len, query_offset, q_start, q_len, (uint16_t*)o, o_stride_h,
       o_stride_t, entries, H, H_KV, block_size, max_blocks, max_q_len, softmax_scale, workspace,
       workspace_bytes, (hipStream_t)stream);
+}
+
+int64_t lse_packed_bf16_weight_bytes(int64_t N, int64_t K) {
+  if (N < 0 || K < 0) return -1;
+  return lse::packed_bf16_bytes(N, K);
+}
+
+int lse_pack_bf16_weight(const void* w, int64_t ldw, int64_t N, int64_t K, void* wp,
+                         void* stream) {
+  if (N < 0 || K < 0 || N > kMaxRows) return LSE_E_SHAPE;
+  if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
+  if (N == 0 || K == 0) return LSE_OK;
+  if (!w || !wp) return LSE_E_NULL;
+  if (int st = check_bf16_matrix(w, ldw, N, K, 8)) return st;
+  if (!aligned(wp, 16)) return LSE_E_ALIGN;
+  if (lse::packed_bf16_bytes(N, K) >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+  return lse::launch_pack_bf16((const uint16_t*)w, ldw, N, K, (uint16_t*)wp, (hipStream_t)stream);
+}
+
+int lse_bf16_decode_gemm(const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy,
+                         int64_t M, int64_t N, int64_t K, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || N > kMaxRows) return LSE_E_SHAPE;
+  if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
+  if (M > LSE_DECODE_MAX_M) return LSE_E_ALGO;
+  if (M == 0 || N == 0) return LSE_OK;
+  if (!wp) return LSE_E_NULL;
+  if (!aligned(wp, 16)) return LSE_E_ALIGN;
+  if (int st = check_bf16_matrix(y, ldy, M, N, 1)) return st;
+  hipStream_t st = (hipStream_t)stream;
+  if (K == 0) return zero_output(y, ldy, M, N, st);
+  if (int e = check_bf16_matrix(x, ldx, M, K, 8)) return e;
+  if (lse::packed_bf16_bytes(N, K) >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+  if (((M - 1) * ldx + K) * 2 >= (int64_t)kBufferLimit) return LSE_E_RANGE;
+  return lse::launch_bf16_skinny((const uint16_t*)x, ldx, (const uint16_t*)wp, (uint16_t*)y, ldy,
+                                 M, N, K, st);
 }
 
 int64_t lse_query(int key) {

@@ -87,6 +87,11 @@ __device__ __forceinline__ i32x4 mfma_i8(uint4 a, uint4 b, i32x4 c) {
 // Gate/up layout of the MLP's fused projection (two (I, K) matrices): row tile 2t holds gate rows
 // 16t..16t+15 and row tile 2t+1 the same rows of up, so 2 ceil(I/16) row tiles in all; a kernel
 // holding an even-aligned pair of row tiles holds matching gate and up rows.
+//
+// bf16 weight layout (the bf16 lm_head): the same 16-row x 64-K steps, each 2 KB: at byte
+// (rb * nsteps + j) * 2048 + 1024 h + 16 l + 2 i lies w[16 rb + l % 16][64 j + 16 (l / 16) +
+// 8 h + i] (zero past N and K): tile h = 0 and 1 are the "lo" and "hi" MFMA operands that
+// dequantizing an int8 tile of the same step yields.
 constexpr int kTileRows = 16;
 constexpr int kTileK = 64;
 constexpr int kTileBytes = 1024;

@@ -60,3 +60,39 @@ int launch_pack_glu(const int8_t* q, int64_t I, int64_t K, int8_t* qp, hipStream
 }
 
 }  // namespace lse
+
+namespace lse {
+
+// Row-major (N, K) bf16 (row stride ldw) -> the bf16 tile layout (lse_common.h). One thread per
+// 16-byte lane slot: 8 K-consecutive bf16 of one row, one aligned 128-bit source load.
+__global__ void __launch_bounds__(256)
+pack_bf16_tiles(const uint16_t* __restrict__ w, int64_t ldw, int N, int K, int nsteps,
+                int64_t slots, uint4* __restrict__ wp) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= slots) return;
+  const int lane = (int)(t & 63);
+  const int h = (int)((t >> 6) & 1);
+  const int64_t step = t >> 7;  // (rb, j)
+  const int64_t rb = step / nsteps;
+  const int j = (int)(step - rb * nsteps);
+  const int64_t row = 16 * rb + (lane & 15);
+  const int k = 64 * j + 16 * (lane >> 4) + 8 * h;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (row < N && k < K) v = *reinterpret_cast<const uint4*>(w + row * ldw + k);
+  wp[t] = v;
+}
+
+int64_t packed_bf16_bytes(int64_t N, int64_t K) {
+  return ceil_div(N, kTileRows) * ceil_div(K, kTileK) * 2 * kTileBytes;
+}
+
+int launch_pack_bf16(const uint16_t* w, int64_t ldw, int64_t N, int64_t K, uint16_t* wp,
+                     hipStream_t stream) {
+  const int64_t slots = packed_bf16_bytes(N, K) / 16;
+  hipLaunchKernelGGL(pack_bf16_tiles, dim3((unsigned)ceil_div(slots, 256)), dim3(256), 0, stream,
+                     w, ldw, (int)N, (int)K, (int)ceil_div(K, kTileK), slots,
+                     reinterpret_cast<uint4*>(wp));
+  return launch_status();
+}
+
+}  // namespace lse

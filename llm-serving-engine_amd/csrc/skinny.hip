@@ -25,6 +25,10 @@
 //    even number of row tiles, so every panel holds matching gate and up rows; the final
 //    reduction adds slice pairs (gate tile, up tile) in one wave, which writes
 //    h = bf16(silu(g) * u) for its I output columns. No K splits.
+//  * bf16 weights (BFW, the lm_head kept in bf16): each 64-wide K step of a row tile is two
+//    1 KB tiles already in bf16 operand form (the "lo" and "hi" halves that dequantization
+//    produces from an int8 tile, layout in lse_common.h), loaded instead of dequantized; no
+//    scales, y = bf16(sum).
 //
 // Activations reach the MFMAs from LDS, never by gathering 16 token rows per load from global
 // memory (that pattern runs at a fraction of the cache bandwidth):
@@ -72,9 +76,9 @@ struct SkinnyArgs {
 };
 
 // Register stage of the weight ring: one 1 KB tile per row tile of the panel.
-template <int RT>
+template <int RT, int WN>
 struct SkinnyWStage {
-  uint4 w[RT];
+  uint4 w[RT * WN];  // WN 1 KB tiles per row tile: 1 (int8) or 2 (bf16 lo, hi)
 };
 
 // XOR swizzle of a streamed activation step image (16 MT token rows of XROW = 64 ESZ bytes,
@@ -97,10 +101,12 @@ __host__ __device__ constexpr int skinny_swz_mask(int chunks_per_row) {
   return ((chunks_per_row & -chunks_per_row) < 16 ? (chunks_per_row & -chunks_per_row) : 16) - 1;
 }
 
-template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU>
+template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU, bool BFW = false>
 __global__ void __launch_bounds__(64 * W)
 skinny_kernel(SkinnyArgs a) {
   using Acc = std::conditional_t<I8, i32x4, f32x4>;
+  static_assert(!BFW || (!I8 && !GLU), "bf16 weights: plain W16A16 only");
+  constexpr int WN = BFW ? 2 : 1;  // 1 KB weight tiles per row tile and step
   constexpr int SLICES = RT * MT;               // 16x16 output tiles of a panel
   constexpr int ESZ = I8 ? 1 : 2;               // activation element bytes
   constexpr int XL = I8 ? 1 : 2;                // 16-byte activation pieces per token tile and step
@@ -116,7 +122,7 @@ skinny_kernel(SkinnyArgs a) {
   constexpr int XROW = 64 * ESZ;                // bytes of one token row of a step
   constexpr int XCH = XROW / 16;                // chunks per row
   constexpr int XI = XLDS ? 0 : MT * ESZ;       // 1 KB pieces per wave per step
-  constexpr int kWaitX = (DX - 1) * (RT + XI);  // loads issued after a step's activations
+  constexpr int kWaitX = (DX - 1) * (RT * WN + XI);  // loads issued after a step's activations
   static_assert(XLDS || kWaitX < 64, "vmcnt holds at most 63");
   // Each ring slot (all waves' parts) is its own array, so the compiler can tell the slot a
   // direct-to-LDS load fills from the slot the MFMAs read, and leaves those waits to the explicit
@@ -155,7 +161,8 @@ skinny_kernel(SkinnyArgs a) {
   const int u_end = (blockIdx.x + 1) * a.units / G;
   const bool split = a.splits > 1;
 
-  const BufferRsrc qres = make_rsrc(a.qp, (uint32_t)a.nrb * (uint32_t)a.nsteps * kTileBytes);
+  const BufferRsrc qres =
+      make_rsrc(a.qp, (uint32_t)a.nrb * (uint32_t)a.nsteps * (uint32_t)(kTileBytes * WN));
   const BufferRsrc xres = make_rsrc(a.x, (uint32_t)(((int64_t)(a.M - 1) * a.ldx + a.K) * ESZ));
   float sxv[MT];
 #pragma unroll
@@ -172,7 +179,7 @@ skinny_kernel(SkinnyArgs a) {
   // Scales are staged per packed row: in the gate/up layout packed row 16 rb + r is gate
   // (rb even) or up (rb odd) row 16 (rb / 2) + r, whose scale is s[(rb & 1) I + 16 (rb / 2) + r].
   const int srow0 = 16 * RT * u_first;
-  const int nsc = split ? 0 : min(16 * RT * u_end, a.N) - srow0;
+  const int nsc = split || BFW ? 0 : min(16 * RT * u_end, a.N) - srow0;
   constexpr int kScPerThread = (kSkinnyScaleLds + 64 * W - 1) / (64 * W);
   float sc_stage[kScPerThread];
 #pragma unroll
@@ -209,13 +216,13 @@ skinny_kernel(SkinnyArgs a) {
       const int r = threadIdx.x + 64 * W * i;
       if (r < kSkinnyScaleLds) s_lds[r] = sc_stage[i];
     }
-    if constexpr (XLDS) __builtin_amdgcn_s_waitcnt(vmcnt_imm((DW - 1) * RT));
+    if constexpr (XLDS) __builtin_amdgcn_s_waitcnt(vmcnt_imm((DW - 1) * RT * WN));
     __syncthreads();
   };
 
   // Weight load cursor: unit lu (panel lp of split lsp), super-step lsu within it.
   int lu = u_first, lp = u_first % a.panels, lsp = u_first / a.panels, lsu = 0;
-  auto load_w = [&](SkinnyWStage<RT>& st) {
+  auto load_w = [&](SkinnyWStage<RT, WN>& st) {
     const int jr = W * lsu + wave;
     const int j = lsp * a.ssteps + jr;
     const bool kv = lu < u_end && jr < a.ssteps && j < a.nsteps;
@@ -223,8 +230,10 @@ skinny_kernel(SkinnyArgs a) {
     for (int rt = 0; rt < RT; ++rt) {
       const int rb = lp * RT + rt;
       const uint32_t off =
-          ((uint32_t)rb * (uint32_t)a.nsteps + (uint32_t)j) * kTileBytes + 16u * lane;
-      st.w[rt] = buffer_load16(qres, kv && rb < a.nrb ? off : kOutOfRange);
+          ((uint32_t)rb * (uint32_t)a.nsteps + (uint32_t)j) * (kTileBytes * WN) + 16u * lane;
+#pragma unroll
+      for (int h = 0; h < WN; ++h)
+        st.w[WN * rt + h] = buffer_load16(qres, kv && rb < a.nrb ? off + kTileBytes * h : kOutOfRange);
     }
     if (++lsu == a.NSU) {
       lsu = 0;
@@ -281,7 +290,7 @@ skinny_kernel(SkinnyArgs a) {
   const int x_m = min(r16, a.M - 1);
   const unsigned char* x_row_base = x_lds + x_m * xrow_bytes;
   const int x_swz = x_m & xswz;
-  auto compute = [&](const SkinnyWStage<RT>& st, int slot, int sp, int su) {
+  auto compute = [&](const SkinnyWStage<RT, WN>& st, int slot, int sp, int su) {
     uint4 xv[MT][XL];
     if constexpr (XLDS) {
       // A padding step past the unit's range or the last K step (NSU is rounded up to the ring
@@ -315,7 +324,14 @@ skinny_kernel(SkinnyArgs a) {
     } else {
       bf16x8 lo[RT], hi[RT];
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) dequant16(st.w[rt], lo[rt], hi[rt]);
+      for (int rt = 0; rt < RT; ++rt) {
+        if constexpr (BFW) {
+          lo[rt] = as_bf16x8(st.w[2 * rt]);
+          hi[rt] = as_bf16x8(st.w[2 * rt + 1]);
+        } else {
+          dequant16(st.w[rt], lo[rt], hi[rt]);
+        }
+      }
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -348,7 +364,7 @@ skinny_kernel(SkinnyArgs a) {
     const int cnt = min(4, a.N - n);
     float sc[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = r < cnt ? s_lds[n + r - srow0] : 0.0f;
+    for (int r = 0; r < 4; ++r) sc[r] = BFW ? 1.0f : r < cnt ? s_lds[n + r - srow0] : 0.0f;
     store_out4<I8>(a.y, a.ldy, a.acc, a.N, m, n, cnt, v, sc, sxv[b], yvec);
   };
   // Gate/up: slice `slice` (an even row tile rt of token tile b) holds gate rows of output
@@ -433,7 +449,7 @@ skinny_kernel(SkinnyArgs a) {
   };
 
   if (u_first >= u_end) return;
-  SkinnyWStage<RT> wr[DW];
+  SkinnyWStage<RT, WN> wr[DW];
   // Prologue in the steady state's issue order (weights of step t + DW - 1, then activations of
   // unit t + DX - 1), so the activation wait count is the same at every step.
 #pragma unroll
@@ -506,9 +522,10 @@ struct SkinnyShape {
   int splits;
 };
 
-template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU = false>
+template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU = false,
+          bool BFW = false>
 static const void* skinny_fn() {
-  return reinterpret_cast<const void*>(&skinny_kernel<I8, MT, RT, W, DW, DX, XLDS, GLU>);
+  return reinterpret_cast<const void*>(&skinny_kernel<I8, MT, RT, W, DW, DX, XLDS, GLU, BFW>);
 }
 
 // Panel height for 17..64 tokens: each panel re-reads the activations from L2, so panels are as
@@ -530,13 +547,14 @@ static bool skinny_split_k(int64_t N, int64_t K) {
 // N counts packed rows (2 x 16 ceil(I / 16) in the gate/up layout, whose panels hold at least
 // one pair of row tiles and are never split over K).
 template <bool I8>
-static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K, bool glu = false) {
+static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K, bool glu = false,
+                                bool nosplit = false) {
   if (M <= 16) {
     const bool fits = M * (size_t)skinny_x_row((int)K, I8 ? 1 : 2) <= (size_t)kSkinnyXLdsBytes;
     return {1, glu ? 2 : 1, 8, 4, fits, 1};
   }
   const int mt = M <= 32 ? 2 : 4;
-  if (!glu && skinny_split_k(N, K)) return {mt, 4, 4, 4, false, 4};
+  if (!glu && !nosplit && skinny_split_k(N, K)) return {mt, 4, 4, 4, false, 4};
   const int rt = std::max(skinny_rt(N), glu ? 2 : 1);
   if (mt == 2) return {2, rt, rt == 4 ? 4 : 8, 4, false, 1};
   // 64 tokens: two waves per SIMD (eight per workgroup, shallower rings) for 32- and 64-row
@@ -544,7 +562,7 @@ static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K, bool glu = fals
   return rt == 1 ? SkinnyShape{4, 1, 4, 4, false, 1} : SkinnyShape{4, rt, 8, 2, false, 1};
 }
 
-template <bool I8, bool GLU = false>
+template <bool I8, bool GLU = false, bool BFW = false>
 static const void* skinny_kernel_for(const SkinnyShape& sh) {
   if constexpr (GLU) {
     if (sh.mt == 1)
@@ -552,17 +570,20 @@ static const void* skinny_kernel_for(const SkinnyShape& sh) {
                      : skinny_fn<I8, 1, 2, 8, 4, 4, false, true>();
   } else {
     if (sh.mt == 1)
-      return sh.xlds ? skinny_fn<I8, 1, 1, 8, 4, 1, true>() : skinny_fn<I8, 1, 1, 8, 4, 4, false>();
+      return sh.xlds ? skinny_fn<I8, 1, 1, 8, 4, 1, true, false, BFW>()
+                     : skinny_fn<I8, 1, 1, 8, 4, 4, false, false, BFW>();
     if (sh.rt == 1)
-      return sh.mt == 2 ? skinny_fn<I8, 2, 1, 8, 4, 4, false>() : skinny_fn<I8, 4, 1, 4, 4, 4, false>();
-    if (sh.mt == 4 && sh.rt == 4 && sh.w == 4) return skinny_fn<I8, 4, 4, 4, 4, 2, false>();
+      return sh.mt == 2 ? skinny_fn<I8, 2, 1, 8, 4, 4, false, false, BFW>()
+                        : skinny_fn<I8, 4, 1, 4, 4, 4, false, false, BFW>();
+    if constexpr (!BFW)
+      if (sh.mt == 4 && sh.rt == 4 && sh.w == 4) return skinny_fn<I8, 4, 4, 4, 4, 2, false>();
   }
   if (sh.mt == 2) {
-    if (sh.rt == 2) return skinny_fn<I8, 2, 2, 8, 4, 2, false, GLU>();
-    return skinny_fn<I8, 2, 4, 4, 4, 4, false, GLU>();
+    if (sh.rt == 2) return skinny_fn<I8, 2, 2, 8, 4, 2, false, GLU, BFW>();
+    return skinny_fn<I8, 2, 4, 4, 4, 4, false, GLU, BFW>();
   }
-  if (sh.rt == 2) return skinny_fn<I8, 4, 2, 8, 2, 2, false, GLU>();
-  return skinny_fn<I8, 4, 4, 8, 2, 2, false, GLU>();
+  if (sh.rt == 2) return skinny_fn<I8, 4, 2, 8, 2, 2, false, GLU, BFW>();
+  return skinny_fn<I8, 4, 4, 8, 2, 2, false, GLU, BFW>();
 }
 
 struct SkinnyPlan {
@@ -607,13 +628,16 @@ static SkinnyPlan skinny_plan_for(const SkinnyShape& sh, const void* fn, int64_t
   return pl;
 }
 
-// glu > 0: the gate/up layout of two (glu, K) matrices (N is then ignored).
+// glu > 0: the gate/up layout of two (glu, K) matrices (N is then ignored). bfw: bf16 weights.
 template <bool I8>
-static SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t glu = 0) {
+static SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t glu = 0,
+                              bool bfw = false) {
   if (glu > 0) N = 2 * kTileRows * ceil_div(glu, kTileRows);
-  const SkinnyShape sh = skinny_shape<I8>(M, N, K, glu > 0);
-  SkinnyPlan pl = skinny_plan_for<I8>(
-      sh, glu > 0 ? skinny_kernel_for<I8, true>(sh) : skinny_kernel_for<I8>(sh), M, N, K);
+  const SkinnyShape sh = skinny_shape<I8>(M, N, K, glu > 0, bfw);
+  const void* fn = glu > 0 ? skinny_kernel_for<I8, true>(sh)
+                   : bfw   ? skinny_kernel_for<false, false, true>(sh)
+                           : skinny_kernel_for<I8>(sh);
+  SkinnyPlan pl = skinny_plan_for<I8>(sh, fn, M, N, K);
   pl.a.glu = (int)glu;
   return pl;
 }
@@ -643,8 +667,8 @@ template <bool I8>
 static int skinny_run(const void* x, int64_t ldx, const int8_t* qp, const float* s,
                       const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
                       int64_t N, int64_t K, int64_t glu, void* ws, int64_t ws_bytes,
-                      hipStream_t stream) {
-  SkinnyPlan pl = skinny_plan<I8>(M, N, K, glu);
+                      hipStream_t stream, bool bfw = false) {
+  SkinnyPlan pl = skinny_plan<I8>(M, N, K, glu, bfw);
   if (ws_bytes < pl.part_bytes || (pl.part_bytes && !ws)) return LSE_E_WORKSPACE;
   SkinnyArgs& a = pl.a;
   a.x = x;
@@ -682,6 +706,16 @@ int launch_w8a8_skinny_glu(const int8_t* xq, const float* sx, const int8_t* qp, 
                            uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
                            hipStream_t stream) {
   return skinny_run<true>(xq, K, qp, s, sx, h, ldh, nullptr, M, 0, K, I, nullptr, 0, stream);
+}
+
+}  // namespace lse
+
+namespace lse {
+
+int launch_bf16_skinny(const uint16_t* x, int64_t ldx, const uint16_t* wp, uint16_t* y,
+                       int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  return skinny_run<false>(x, ldx, reinterpret_cast<const int8_t*>(wp), nullptr, nullptr, y, ldy,
+                           nullptr, M, N, K, 0, nullptr, 0, stream, true);
 }
 
 }  // namespace lse

@@ -17,6 +17,9 @@ import torch
 from . import _lib
 
 __all__ = [
+    "bf16_decode_linear",
+    "pack_bf16_weight",
+    "packed_bf16_shape",
     "paged_attention_forward",
     "pack_glu",
     "pack_weight",
@@ -392,3 +395,42 @@ def rmsnorm_quantize(
         "lse_rmsnorm_quantize",
     )
     return xq, sx, normed
+
+
+def packed_bf16_shape(n: int, k: int) -> tuple[int, int, int]:
+    return ((n + 15) // 16, (k + 63) // 64, 1024)
+
+
+def pack_bf16_weight(w: torch.Tensor) -> torch.Tensor:
+    """Row-major (N, K) bf16 → the bf16 tile layout, a (ceil(N/16), ceil(K/64), 1024) bf16
+    tensor (2 KB per 16-row x 64-K step: the lo and hi MFMA operands), on the GPU."""
+    _require(w.dim() == 2 and w.dtype == torch.bfloat16, "w must be a 2-D bf16 tensor")
+    dev = _on_gpu(w)
+    n, k = w.shape
+    w2 = w if w.stride(1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0 else w.contiguous()
+    wp = torch.empty(packed_bf16_shape(n, k), dtype=torch.bfloat16, device=dev)
+    _lib.check(_lib.library().lse_pack_bf16_weight(w2.data_ptr(), w2.stride(0), n, k,
+                                                    wp.data_ptr(), _stream(dev)),
+               "lse_pack_bf16_weight")
+    return wp
+
+
+def bf16_decode_linear(x: torch.Tensor, wp: torch.Tensor, n: int) -> torch.Tensor:
+    """y = bf16(x · wᵀ) for x (..., K) bf16 with at most 64 rows, w given packed
+    (`pack_bf16_weight`) → y (..., N) bf16; fp32 accumulation."""
+    dev = _on_gpu(x, wp)
+    _require(x.dtype == torch.bfloat16, f"expects bf16 activations, got {x.dtype}")
+    k = x.shape[-1]
+    _require(wp.dtype == torch.bfloat16 and tuple(wp.shape) == packed_bf16_shape(n, k),
+             f"packed weight has shape {tuple(wp.shape)}, (N, K) = ({n}, {k}) needs "
+             f"{packed_bf16_shape(n, k)}")
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    _lib.check(
+        _lib.library().lse_bf16_decode_gemm(x2.data_ptr(), x2.stride(0) if m > 1 else k,
+                                            wp.data_ptr(), y.data_ptr(), n, m, n, k,
+                                            _stream(dev)),
+        "lse_bf16_decode_gemm",
+    )
+    return y.view(*x.shape[:-1], n)

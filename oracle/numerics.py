@@ -303,3 +303,25 @@ def rmsnorm_bf16(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarr
     h = bf16_bits_to_f32(f32_to_bf16_bits((x * r[:, None]).astype(np.float32)))
     w = bf16_bits_to_f32(np.asarray(w_bits, np.uint16))
     return f32_to_bf16_bits((w[None, :] * h).astype(np.float32))
+
+
+# ---- bf16 decode GEMM (the lm_head kept in bf16) -------------------------------------------
+
+
+def pack_bf16_weight(w_bits: np.ndarray) -> np.ndarray:
+    """Row-major (N, K) bf16 bits → the bf16 tile layout, (ceil(N/16), ceil(K/64), 2, 64, 8)
+    uint16: step (rb, j) half h, lane l, element i = w[16 rb + l % 16][64 j + 16 (l // 16) +
+    8 h + i], zero past N and K. A storage permutation of this build's own."""
+    w = np.asarray(w_bits, np.uint16)
+    n, k = w.shape
+    nrb, steps = -(-n // 16), -(-k // 64)
+    padded = np.zeros((nrb * 16, steps * 64), np.uint16)
+    padded[:n, :k] = w
+    # [rb][row r][step j][group g][half h][i] -> [rb][j][h][g][r][i]
+    t = padded.reshape(nrb, 16, steps, 4, 2, 8).transpose(0, 2, 4, 3, 1, 5)
+    return np.ascontiguousarray(t).reshape(nrb, steps, 2, 64, 8)
+
+
+def bf16_linear_golden(x_bits: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
+    """fp64 x · wᵀ of bf16 operands (every product exact in fp64)."""
+    return bf16_bits_to_f32(x_bits).astype(np.float64) @ bf16_bits_to_f32(w_bits).astype(np.float64).T

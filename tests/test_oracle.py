@@ -529,3 +529,34 @@ def test_rmsnorm_matches_llama_rmsnorm():
         np.ones(k, np.float32)), 1e-5))
     vb = float(ora.bf16_bits_to_f32(ora.f32_to_bf16_bits(v))[0, 0])
     np.testing.assert_allclose(h[0, 0], vb / np.sqrt(vb * vb + 1e-5), rtol=2 ** -7)
+
+
+def test_pack_bf16_weight_matches_the_layout_definition():
+    """Brute force over the definition (ragged N and K), and a tile walk: the lo/hi operand pairs
+    of every step, contracted with the matching activation slices, give x · wᵀ."""
+    rng = np.random.default_rng(12)
+    n, k = 20, 80
+    w = ora.f32_to_bf16_bits(rng.standard_normal((n, k), dtype=np.float32))
+    p = ora.pack_bf16_weight(w)
+    assert p.shape == (2, 2, 2, 64, 8)
+    for rb in range(2):
+        for j in range(2):
+            for h in range(2):
+                for lane in range(64):
+                    for i in range(8):
+                        r, c = 16 * rb + lane % 16, 64 * j + 16 * (lane // 16) + 8 * h + i
+                        want = w[r, c] if r < n and c < k else 0
+                        assert p[rb, j, h, lane, i] == want
+    x = ora.f32_to_bf16_bits(rng.standard_normal((3, k), dtype=np.float32))
+    xf = np.zeros((3, 128))
+    xf[:, :k] = ora.bf16_bits_to_f32(x)
+    pf = ora.bf16_bits_to_f32(p)
+    y = np.zeros((3, 32))
+    for rb in range(2):
+        for j in range(2):
+            for lane in range(64):
+                r, g = lane % 16, lane // 16
+                for h in range(2):
+                    cols = 64 * j + 16 * g + 8 * h + np.arange(8)
+                    y[:, 16 * rb + r] += xf[:, cols] @ pf[rb, j, h, lane].astype(np.float64)
+    np.testing.assert_allclose(y[:, :n], ora.bf16_linear_golden(x, w), rtol=1e-12, atol=1e-12)
