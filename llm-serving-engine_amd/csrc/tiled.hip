@@ -2,7 +2,7 @@
 //   W8A16: y[m,n] = bf16(s[n] * sum_k x[m,k] q[n,k])               bf16 x, fp32 accumulation
 //   W8A8:  acc[m,n] = sum_k xq[m,k] q[n,k] exactly in int32;  y = bf16((acc * sx[m]) * s[n])
 //
-// MFMA-bound. A block of WGM x WGN = 2 x 4 waves (two per SIMD, so one wave's LDS reads and
+// MFMA-bound. A block of WGM x WGN = 8 waves (two per SIMD, so one wave's LDS reads and
 // dequantization overlap the other's MFMAs) computes a BM (tokens) x BN (weight rows) tile of y
 // over K in 64-wide steps; wave (wm, wn) owns a WM x WN sub-tile (128 x 64 for the big tile) of
 // 16x16 MFMA tiles whose A operand is a packed 1 KB weight tile (16 rows x 64 K-bytes, already
@@ -61,8 +61,7 @@ struct TiledArgs {
 };
 
 constexpr int kGroupM = 4;
-constexpr int kTiledWgm = 2, kTiledWgn = 4;
-constexpr int kTiledThreads = 64 * kTiledWgm * kTiledWgn;
+constexpr int kTiledThreads = 512;  // 8 waves in every wave layout
 
 template <bool I8>
 __device__ __forceinline__ int tiled_swz(int r) {
@@ -277,10 +276,14 @@ struct TiledShape {
 template <bool I8, int BM, int BN, bool GLU>
 static const void* tiled_fn() {
   // LDS per block: NST x (x stage + weight stage) <= 160 KB; 128 x 128 tiles keep two blocks
-  // per CU.
+  // per CU. Wave layout 2 x 4, except the W8A16 128 x 256 tile: there 1 x 8 (128 x 32 per wave)
+  // dequantizes each weight tile in one wave instead of two, 9-12% faster on MI355X; in W8A8
+  // (no dequantization) 2 x 4 stays faster (fewer x fragment reads per MFMA).
   constexpr int nst = I8 ? 4 : 3;
+  constexpr int wgm = (!I8 && BM == 128 && BN == 256) ? 1 : 2;
+  static_assert(64 * wgm * (8 / wgm) == kTiledThreads, "8 waves");
   return reinterpret_cast<const void*>(
-      &tiled_gemm_kernel<I8, BM, BN, kTiledWgm, kTiledWgn, nst, GLU>);
+      &tiled_gemm_kernel<I8, BM, BN, wgm, 8 / wgm, nst, GLU>);
 }
 
 template <bool I8, bool GLU>
@@ -291,21 +294,24 @@ static const void* tiled_kernel_for(const TiledShape& sh) {
   return tiled_fn<I8, 128, 128, GLU>();
 }
 
-// The tile that minimizes (rounds of resident blocks) x (CU time per round) = rounds x tile area
-// x blocks per CU / relative efficiency: big tiles need fewer LDS bytes per MFMA, small tiles fill
-// the CUs when there are few tiles. Efficiencies relative to 256 x 256, measured on MI355X at
-// M = 8192 (many rounds).
+// The tile that minimizes the time of the busiest CU: ceil(tiles / CUs) x tile area / relative
+// efficiency (big tiles need fewer LDS bytes per MFMA; small tiles fill the CUs when there are
+// few tiles). A 128 x 128 tile keeps two blocks per CU, so its efficiency is the one measured
+// with two resident. Efficiencies relative to 256 x 256, measured on MI355X at M = 8192 (many
+// rounds), per mode; this picks the fastest of the four tiles on each of the 18 Llama-3-8B
+// prefill shapes timed (qkv, o_proj, gate_up, down at M = 512 and 2048, gate_up at 8192; both
+// modes).
+template <bool I8>
 static TiledShape tiled_shape(int64_t M, int64_t N, int cus) {
   static const TiledShape cand[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
-  static const double eff[] = {1.0, 0.79, 0.85, 0.85};
-  static const int per_cu[] = {1, 1, 1, 2};
+  static const double eff16[] = {1.0, 0.84, 0.865, 0.85};
+  static const double eff8[] = {1.0, 0.81, 0.865, 0.86};
+  const double* eff = I8 ? eff8 : eff16;
   TiledShape best = cand[0];
   double best_cost = 1e300;
   for (int i = 0; i < 4; ++i) {
     const int64_t blocks = ceil_div(M, cand[i].bm) * ceil_div(N, cand[i].bn);
-    const int64_t rounds = ceil_div(blocks, (int64_t)cus * per_cu[i]);
-    const int64_t sharing = std::min<int64_t>(per_cu[i], ceil_div(blocks, cus));  // blocks per CU
-    const double cost = (double)rounds * cand[i].bm * cand[i].bn * sharing / eff[i];
+    const double cost = (double)ceil_div(blocks, (int64_t)cus) * cand[i].bm * cand[i].bn / eff[i];
     if (cost < best_cost * 0.999) {
       best_cost = cost;
       best = cand[i];
@@ -330,7 +336,7 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
                         const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
                         int64_t N, int64_t K, int64_t glu, hipStream_t stream) {
   if (glu > 0) N = 2 * kTileRows * ceil_div(glu, kTileRows);
-  const TiledShape sh = tiled_shape(M, N, device_cus());
+  const TiledShape sh = tiled_shape<I8>(M, N, device_cus());
   TiledArgs a{};
   a.x = x;
   a.ldx = ldx;
