@@ -1,6 +1,7 @@
 """Benchmark of the int8 quantized Linear forward on one MI355X.
 
-Headline (`value`): config 1, the W8A16 decode sweep. One step runs the decode kernel over the
+Headline (`value`): config 1, the W8A16 decode sweep. One step runs the decode path (the decode
+kernel; for gate_up at 64 tokens a 64 x 128 tile of the tiled kernel) over the
 four Llama-3-8B linear shapes (K, N) in {(4096, 6144) fused QKV, (4096, 4096) o_proj,
 (4096, 28672) fused gate_up, (14336, 4096) down} at M in {1, 8, 32, 64}, over LAYERS distinct
 copies of the weights (LAYERS x 218 MB, far beyond the 256 MB Infinity Cache, so every launch
@@ -408,11 +409,12 @@ SWEEP_CALLS = [(m, si) for m in DECODE_MS for _ in range(LAYERS) for si in range
 
 def _decode_calls(records: list[dict]) -> list[list[dict]]:
     """Dispatch records (in dispatch order) grouped into decode GEMM calls: a skinny_kernel
-    dispatch, plus the skinny_reduce dispatch that follows it when K is split."""
+    dispatch, plus the skinny_reduce dispatch that follows it when K is split, or the 64 x 128
+    tiled_gemm_kernel dispatch the decode path uses for gate_up at 33..64 tokens."""
     calls: list[list[dict]] = []
     for r in records:
         name = r["Kernel_Name"]
-        if "skinny_kernel" in name:
+        if "skinny_kernel" in name or "tiled_gemm_kernel" in name:
             calls.append([r])
         elif "skinny_reduce" in name:
             calls[-1].append(r)
@@ -472,7 +474,8 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> None:
         "python3 bench.py --summarize-profiles gpurun_out/prof_decode gpurun_out/pmc_fetch "
         "gpurun_out/pmc_write",
     ]
-    out = ["# skinny_kernel (+ skinny_reduce) — config-1 W8A16 decode sweep", "",
+    out = ["# skinny_kernel (+ skinny_reduce; tiled_gemm_kernel 64 x 128 for gate_up at 64 "
+           "tokens) — config-1 W8A16 decode sweep", "",
            "Llama-3-8B shapes (K, N) in {(4096,6144), (4096,4096), (4096,28672), (14336,4096)} x "
            f"M in {DECODE_MS}, {LAYERS} weight copies rotated, one MI355X.", "",
            "Commands (repository root, one MI355X; the last runs on any host):", "", "```",
@@ -480,11 +483,12 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> None:
            "## rocprofv3 --stats (whole profiled run)", "",
            "| kernel | calls | avg us | total ms |", "|---|---|---|---|"]
     for r in stats:
-        if "skinny" in r["Name"] or "bitwise_not" in r["Name"]:
+        if any(t in r["Name"] for t in ("skinny", "tiled_gemm_kernel", "bitwise_not")):
             out.append(f"| `{_short(r['Name'])[:90]}` | {r['Calls']} | "
                        f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['TotalDurationNs']) / 1e6:.2f} |")
     out += ["", f"## Per call (median over {len(replays)} replays of the sweep graph; a call is the "
-            "skinny_kernel dispatch plus, when K is split, its skinny_reduce)", "",
+            "skinny_kernel dispatch plus, when K is split, its skinny_reduce, or one "
+            "tiled_gemm_kernel dispatch)", "",
             "HBM bytes = FETCH_SIZE x 1024 x "
             f"{ff:.3f} + WRITE_SIZE x 1024 x {wf:.3f}: the 64 MiB calibration copy read "
             f"{fkib:.1f} KiB of FETCH_SIZE and {wkib:.1f} KiB of WRITE_SIZE.", "",

@@ -171,14 +171,19 @@ def test_output_stride_guard_band(pkg, dev, algo):
     assert ok, msg
 
 
-def test_decode_rows_are_batch_invariant(pkg, dev):
-    """A row's result does not depend on the other rows of its token class."""
-    i, k = 300, 1024
+@pytest.mark.parametrize("i,k", [(300, 1024), (8200, 144)])
+def test_decode_rows_are_batch_invariant(pkg, dev, i, k):
+    """A row's result does not depend on the other rows of its token class. I = 8200 (1026 packed
+    row tiles) sends 33..64 tokens to the 64 x 128 tiled route; it is also checked against the
+    golden there."""
     x_bits, q, s = _inputs(31, 64, i, k)
     for lo, hi in ((1, 16), (17, 32), (33, 64)):
         full = _w8a16(pkg, dev, x_bits[:hi], q, s, DECODE)
         part = _w8a16(pkg, dev, x_bits[:lo], q, s, DECODE)
         np.testing.assert_array_equal(part, full[:lo], err_msg=f"class {lo}..{hi}")
+        if hi == 64:
+            ok, msg = ora.within_tolerance(full, ora.w8a16_glu_golden(x_bits, q, s))
+            assert ok, f"I={i} K={k} M=64: {msg}"
 
 
 def test_rejections(pkg, dev):

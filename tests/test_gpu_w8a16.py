@@ -111,10 +111,13 @@ def test_decode_rejects_a_short_workspace(pkg, dev):
 
 
 @pytest.mark.parametrize(
-    "n,k", [(1, 16), (15, 48), (16, 64), (17, 80), (100, 112), (33, 2064), (64, 4096 + 48)]
+    "n,k", [(1, 16), (15, 48), (16, 64), (17, 80), (100, 112), (33, 2064), (64, 4096 + 48),
+            (16392, 80)]
 )
 def test_decode_ragged_shapes(pkg, dev, n, k):
-    """N not a multiple of 16, K tails of 16/48 past the 64-wide superstep."""
+    """N not a multiple of 16, K tails of 16/48 past the 64-wide superstep. (16392, 80): a weight
+    wide enough (1025 row tiles) that 33..64 tokens take the 64 x 128 tiled route, with a partial
+    last tile and a K tail."""
     for m in (1, 5, 40):
         _check(pkg, dev, m, n, k, 7 * n + k, DECODE)
 
@@ -168,7 +171,7 @@ def test_output_stride_guard_band(pkg, dev, algo):
     assert ora.within_tolerance(y, ora.w8a16_golden(x_bits, q, s))[0]
 
 
-@pytest.mark.parametrize("k,n", [(4096, 512), (14336, 4096), (1024, 6144)])
+@pytest.mark.parametrize("k,n", [(4096, 512), (14336, 4096), (1024, 6144), (256, 16400)])
 def test_decode_rows_are_batch_invariant(pkg, dev, k, n):
     """A row's result does not depend on M or on the other rows within a token class (M <= 16,
     17..32, 33..64): the graphed decode runs a padded power-of-two bucket while eager decode runs
