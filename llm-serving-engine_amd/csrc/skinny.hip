@@ -25,9 +25,9 @@
 //    even number of row tiles, so every panel holds matching gate and up rows; the final
 //    reduction adds slice pairs (gate tile, up tile) in one wave, which writes
 //    h = bf16(silu(g) * u) for its I output columns. No K splits.
-//  * W8A16 with 33..64 tokens over a wide weight (at least 1024 row tiles, the MLP gate/up) does
-//    not run here: the decode dispatch sends it to a 64 x 128 tile of the tiled kernel
-//    (skinny_wide_tiled).
+//  * W8A16 with 17..64 tokens over a wide weight (at least 1024 row tiles, the MLP gate/up) does
+//    not run here: the decode dispatch sends it to a 32 x 128 or 64 x 128 tile of the tiled
+//    kernel (skinny_wide_tiled).
 //  * bf16 weights (BFW, the lm_head kept in bf16): each 64-wide K step of a row tile is two
 //    1 KB tiles already in bf16 operand form (the "lo" and "hi" halves that dequantization
 //    produces from an int8 tile, layout in lse_common.h), loaded instead of dequantized; no
@@ -670,13 +670,14 @@ int launch_w8a16_wide_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, c
                              uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                              int64_t glu, hipStream_t stream);  // tiled.hip
 
-// W8A16 with 33..64 tokens over a wide weight (64-row panels in this kernel, never split): the
-// 64 x 128 tiled kernel instead. Here this kernel's waves split each panel's K steps and then add
-// 16 partial tiles each through LDS; at 64 tokens that reduction and the per-wave activation
-// ring cost more than they save, while a tile over the whole K shares one activation stage
-// among its waves. Chosen by the token class and N only, like every decode configuration.
+// W8A16 with 17..64 tokens over a wide weight (64-row panels in this kernel, never split): a
+// 32 x 128 or 64 x 128 tile of the tiled kernel instead. Here this kernel's waves split each
+// panel's K steps and then add 8 or 16 partial tiles each through LDS; with 17 or more tokens
+// that reduction and the per-wave activation rings cost more than they save, while a tile over
+// the whole K shares one activation stage among its waves. Chosen by the token class and N only,
+// like every decode configuration.
 static bool skinny_wide_tiled(int64_t M, int64_t N) {
-  return M > 32 && ceil_div(N, kTileRows) >= 1024;
+  return M > 16 && ceil_div(N, kTileRows) >= 1024;
 }
 
 template <bool I8>

@@ -289,9 +289,11 @@ static const void* tiled_fn() {
 template <bool I8, bool GLU>
 static const void* tiled_kernel_for(const TiledShape& sh) {
   if constexpr (!I8) {
-    // 33..64 tokens over a wide weight (launch_w8a16_wide_decode): four waves of 64 x 32.
+    // 17..64 tokens over a wide weight (launch_w8a16_wide_decode): four waves of BM x 32.
     if (sh.bm == 64)
       return reinterpret_cast<const void*>(&tiled_gemm_kernel<false, 64, 128, 1, 4, 4, GLU>);
+    if (sh.bm == 32)
+      return reinterpret_cast<const void*>(&tiled_gemm_kernel<false, 32, 128, 1, 4, 4, GLU>);
   }
   if (sh.bm == 256 && sh.bn == 256) return tiled_fn<I8, 256, 256, GLU>();
   if (sh.bm == 256 && sh.bn == 128) return tiled_fn<I8, 256, 128, GLU>();
@@ -336,15 +338,17 @@ static int device_cus() {
 }
 
 // glu > 0: the gate/up layout of two (glu, K) matrices, N = 2 x 16 ceil(glu / 16) packed rows.
-// `wide_decode`: the 64 x 128 tile of launch_w8a16_wide_decode instead of the cost model's.
+// `wide_decode`: the 32 x 128 or 64 x 128 tile of launch_w8a16_wide_decode instead of the cost
+// model's.
 template <bool I8>
 static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const float* s,
                         const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
                         int64_t N, int64_t K, int64_t glu, hipStream_t stream,
                         bool wide_decode = false) {
   if (glu > 0) N = 2 * kTileRows * ceil_div(glu, kTileRows);
-  const TiledShape sh = wide_decode ? TiledShape{64, 128} : tiled_shape<I8>(M, N, device_cus());
-  const int threads = sh.bm == 64 ? 256 : kTiledThreads;
+  const TiledShape sh = wide_decode ? TiledShape{M > 32 ? 64 : 32, 128}
+                                    : tiled_shape<I8>(M, N, device_cus());
+  const int threads = sh.bm <= 64 ? 256 : kTiledThreads;
   TiledArgs a{};
   a.x = x;
   a.ldx = ldx;
@@ -377,12 +381,13 @@ int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* qp, const fl
   return launch_tiled<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, 0, stream);
 }
 
-// The decode kernel's 33..64-token class over a wide weight (the MLP gate/up projection, fused or
-// not; chosen by the decode dispatch). Each block owns a 64 x 128 output tile over the whole K,
-// so there is no cross-wave reduction of K partial sums, and its four waves share one activation
-// stage per K step through LDS. On MI355X this takes 33 us against 41 us for the decode kernel
-// on gate_up (K 4096, N 28672) at 64 tokens. Every output is the K steps summed in increasing
-// order, as for every tile shape, so rows do not depend on M or on the other rows.
+// The decode kernel's 17..32- and 33..64-token classes over a wide weight (the MLP gate/up
+// projection, fused or not; chosen by the decode dispatch). Each block owns a 32 x 128 or
+// 64 x 128 output tile (the class's padded token count) over the whole K, so there is no
+// cross-wave reduction of K partial sums, and its four waves share one activation stage per K
+// step through LDS. On MI355X, gate_up (K 4096, N 28672) takes 26 us against 31 us for the
+// decode kernel at 32 tokens, and 33 us against 41 us at 64. Every output is the K steps summed
+// in increasing order, as for every tile shape, so rows do not depend on M or on the other rows.
 int launch_w8a16_wide_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
                              uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                              int64_t glu, hipStream_t stream) {

@@ -116,9 +116,9 @@ def test_decode_rejects_a_short_workspace(pkg, dev):
 )
 def test_decode_ragged_shapes(pkg, dev, n, k):
     """N not a multiple of 16, K tails of 16/48 past the 64-wide superstep. (16392, 80): a weight
-    wide enough (1025 row tiles) that 33..64 tokens take the 64 x 128 tiled route, with a partial
-    last tile and a K tail."""
-    for m in (1, 5, 40):
+    wide enough (1025 row tiles) that 17..64 tokens take the 32 x 128 or 64 x 128 tiled route,
+    with a partial last tile and a K tail."""
+    for m in (1, 5, 20, 40):
         _check(pkg, dev, m, n, k, 7 * n + k, DECODE)
 
 
