@@ -86,12 +86,12 @@ struct SkinnyWStage {
 
 // XOR swizzle of a streamed activation step image (16 MT token rows of XROW = 64 ESZ bytes,
 // 16-byte chunks): chunk c of row m sits at c ^ xstep_swz(m). A fragment read takes one logical
-// chunk of 16 consecutive rows; rows are 128 (bf16) or 64 (int8) bytes, so 2 or 4 consecutive
-// rows share a 256-byte bank line, and the swizzle varies with m >> 1 (m >> 2) to give those 16
-// rows 16 distinct bank groups.
+// chunk of 16 consecutive rows; rows are 128 (bf16) or 64 (int8) bytes. Measured on MI355X with
+// SQ_LDS_BANK_CONFLICT, these swizzles read with no conflict (the same ones as the tiled
+// kernel's): bf16 (m & 7) ^ ((m >> 3) & 1), int8 (m >> 1) & 3.
 template <int ESZ>
 __host__ __device__ constexpr int xstep_swz(int m) {
-  return ESZ == 2 ? (m >> 1) & 7 : (m >> 2) & 3;
+  return ESZ == 2 ? (m & 7) ^ ((m >> 3) & 1) : (m >> 1) & 3;
 }
 
 // Bytes of one whole-staged activation row: K rounded up to whole 64-wide steps.

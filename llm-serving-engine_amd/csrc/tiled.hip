@@ -18,8 +18,8 @@
 //  * Weights stay int8 in LDS (half the footprint and fill traffic of bf16); in W8A16 each wave
 //    dequantizes its WN/16 tiles after the LDS read (exact: |q| <= 127), 1.5 VALU ops per
 //    weight, shared by the WM/16 token tiles it multiplies.
-//  * x rows are stored 16-byte-chunk swizzled (chunk c of row r at c ^ swz(r)) so the 16 rows a
-//    fragment read touches at one K offset fall into distinct banks.
+//  * x rows are stored 16-byte-chunk swizzled (chunk c of row r at c ^ swz(r)) so the fragment
+//    reads of 16 rows at one K offset have no LDS bank conflicts (tiled_swz).
 //  * One barrier per stage: after it, the stage's loads from every wave have landed and every
 //    wave has finished reading the slot the next loads overwrite.
 //
@@ -65,9 +65,12 @@ constexpr int kTiledThreads = 512;  // 8 waves in every wave layout
 
 template <bool I8>
 __device__ __forceinline__ int tiled_swz(int r) {
-  // bf16 rows are 128 bytes (8 chunks, half the banks): rows 2i and 2i+1 cover both halves, so
-  // (r >> 1) spreads 16 rows over all 64 banks. int8 rows are 64 bytes (4 chunks, a quarter).
-  return I8 ? (r >> 2) & 3 : (r >> 1) & 7;
+  // A fragment read (ds_read_b128) takes one logical chunk of 16 consecutive rows per lane
+  // group. Measured on MI355X with SQ_LDS_BANK_CONFLICT, these swizzles read with no conflict:
+  // bf16 rows (128 bytes, 8 chunks) (r & 7) ^ ((r >> 3) & 1), int8 rows (64 bytes, 4 chunks)
+  // (r >> 1) & 3. (The (r >> 1) & 7 and (r >> 2) & 3 spreads, conflict-free on a plain model of
+  // 64 four-byte banks served 16 lanes at a time, cost 4 conflict cycles per read.)
+  return I8 ? (r >> 1) & 3 : (r & 7) ^ ((r >> 3) & 1);
 }
 
 template <bool I8, int BM, int BN, int WGM, int WGN, int NST, bool GLU>
@@ -130,10 +133,10 @@ tiled_gemm_kernel(TiledArgs a) {
 
   // Lane l of load i of a stage fills byte 1024 (wave + W i) + 16 l of the slot's x image: row
   // r = RPL (wave + W i) + l / XCH (RPL = 1024 / XROW rows per load), physical chunk l % XCH,
-  // which holds logical chunk (l % XCH) ^ swz(r). W RPL is a multiple of 8, so swz(r) is the same
+  // which holds logical chunk (l % XCH) ^ swz(r). W RPL is a multiple of 16, so swz(r) is the same
   // for every i and the lane's K byte is fixed; only the row moves, by W RPL per load.
   constexpr int RPL = 1024 / XROW;
-  static_assert((W * RPL) % 8 == 0, "swizzle must not depend on the load index");
+  static_assert((W * RPL) % 16 == 0, "swizzle must not depend on the load index");
   const int x_r0 = RPL * wave + lane / XCH;
   const int x_kb = 16 * ((lane % XCH) ^ tiled_swz<I8>(x_r0));
   const int64_t x_step = (int64_t)W * RPL * a.ldx * ESZ;
