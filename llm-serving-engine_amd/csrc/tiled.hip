@@ -279,11 +279,13 @@ struct TiledShape {
 template <bool I8, int BM, int BN, bool GLU>
 static const void* tiled_fn() {
   // LDS per block: NST x (x stage + weight stage) <= 160 KB; 128 x 128 tiles keep two blocks
-  // per CU. Wave layout 2 x 4, except the W8A16 128 x 256 tile: there 1 x 8 (128 x 32 per wave)
-  // dequantizes each weight tile in one wave instead of two, 9-12% faster on MI355X; in W8A8
-  // (no dequantization) 2 x 4 stays faster (fewer x fragment reads per MFMA).
+  // per CU. Wave layout 2 x 4, except the W8A16 tiles 256 wide: there 1 x 8 (BM x 32 per wave)
+  // dequantizes each weight tile in one wave instead of two, on MI355X 2-9 % faster for
+  // 256 x 256 and 9-12 % for 128 x 256 (it reads twice the x fragments, which the conflict-free
+  // swizzle and LDS's 256 bytes per clock of b128 reads absorb). In W8A8 (no dequantization)
+  // 2 x 4 stays faster.
   constexpr int nst = I8 ? 4 : 3;
-  constexpr int wgm = (!I8 && BM == 128 && BN == 256) ? 1 : 2;
+  constexpr int wgm = (!I8 && BN == 256) ? 1 : 2;
   static_assert(64 * wgm * (8 / wgm) == kTiledThreads, "8 waves");
   return reinterpret_cast<const void*>(
       &tiled_gemm_kernel<I8, BM, BN, wgm, 8 / wgm, nst, GLU>);
@@ -314,7 +316,7 @@ static const void* tiled_kernel_for(const TiledShape& sh) {
 template <bool I8>
 static TiledShape tiled_shape(int64_t M, int64_t N, int cus) {
   static const TiledShape cand[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
-  static const double eff16[] = {1.0, 0.84, 0.865, 0.85};
+  static const double eff16[] = {1.0, 0.86, 0.87, 0.835};
   static const double eff8[] = {1.0, 0.81, 0.865, 0.86};
   const double* eff = I8 ? eff8 : eff16;
   TiledShape best = cand[0];
