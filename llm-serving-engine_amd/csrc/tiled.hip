@@ -283,8 +283,9 @@ static const void* tiled_fn() {
   // dequantizes each weight tile in one wave instead of two, on MI355X 2-9 % faster for
   // 256 x 256 and 9-12 % for 128 x 256 (it reads twice the x fragments, which the conflict-free
   // swizzle and LDS's 256 bytes per clock of b128 reads absorb). In W8A8 (no dequantization)
-  // 2 x 4 stays faster.
-  constexpr int nst = I8 ? 4 : 3;
+  // 2 x 4 stays faster. Stage slots: 3 for bf16 x (4 would not fit the 256 x 256 tile, and
+  // measured no faster on the others), 4 for int8 x except the 256 x 256 tile (3: 1-7 % faster).
+  constexpr int nst = (I8 && !(BM == 256 && BN == 256)) ? 4 : 3;
   constexpr int wgm = (!I8 && BN == 256) ? 1 : 2;
   static_assert(64 * wgm * (8 / wgm) == kTiledThreads, "8 waves");
   return reinterpret_cast<const void*>(
