@@ -108,7 +108,8 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 //   r = 1 / sqrt(fl32(sum_k x^2 / K) + eps),  h_k = bf16(w_k * bf16(x_k * r))
 // then sx = fl32(amax_k |h_k| / 127) and xq_k = clamp(rne(h_k / sx), -127, 127), exactly as
 // quantize_act_rows does for an existing bf16 row. One workgroup per token; the row is read three
-// times (sum of squares, amax, quantize), the last two from L2. `normed` (optional) receives h.
+// times (sum of squares, amax, quantize), the last two from L2 (rows longer than 8192 elements;
+// shorter ones take rmsnorm_quant_rows_reg). `normed` (optional) receives h.
 __device__ __forceinline__ float rms_h(uint32_t xb, uint32_t wb, float r) {
   const float x = __builtin_bit_cast(float, xb);
   const float h = bf16_to_f32(f32_to_bf16(x * r));
@@ -171,11 +172,89 @@ rmsnorm_quant_rows(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* 
   }
 }
 
+// The same for rows of at most NV x 2048 elements (hidden sizes up to 8192): thread t keeps
+// elements 8 t + 2048 i (i < NV) of x and of the weight in registers, so the row is read once and
+// the normed row is quantized from registers. Slots past K hold zeros, which add exact zeros to
+// the sum of squares and to nothing else; the arithmetic and every order of summation are those
+// of rmsnorm_quant_rows, so the results are bit-identical.
+template <int NV>
+__global__ void __launch_bounds__(kQuantThreads)
+rmsnorm_quant_rows_reg(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
+                       float eps, int8_t* __restrict__ xq, float* __restrict__ sx,
+                       uint16_t* __restrict__ normed, int K) {
+  __shared__ float red[kQuantThreads / 64];
+  const int64_t m = blockIdx.x;
+  const uint16_t* row = x + m * ldx;
+  uint32_t u[NV][4], gw[NV][4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
+    const uint4 v = k < K ? *reinterpret_cast<const uint4*>(row + k) : make_uint4(0, 0, 0, 0);
+    const uint4 g = k < K ? *reinterpret_cast<const uint4*>(w + k) : make_uint4(0, 0, 0, 0);
+    u[i][0] = v.x, u[i][1] = v.y, u[i][2] = v.z, u[i][3] = v.w;
+    gw[i][0] = g.x, gw[i][1] = g.y, gw[i][2] = g.z, gw[i][3] = g.w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = __builtin_bit_cast(float, u[i][j] << 16);
+      const float b = __builtin_bit_cast(float, u[i][j] & 0xffff0000u);
+      ss = __builtin_fmaf(a, a, ss);
+      ss = __builtin_fmaf(b, b, ss);
+    }
+  }
+  const float var = block_sum(ss, red) / (float)K;
+  const float r = 1.0f / __builtin_sqrtf(var + eps);
+  float amax = 0.0f;
+  uint32_t hb[NV][4];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = rms_h(u[i][j] << 16, gw[i][j] << 16, r);
+      const float hi = rms_h(u[i][j] & 0xffff0000u, gw[i][j] & 0xffff0000u, r);
+      amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
+      hb[i][j] = pack_bf16x2(lo, hi);
+    }
+    if (normed && k < K)
+      *reinterpret_cast<uint4*>(normed + m * K + k) = make_uint4(hb[i][0], hb[i][1], hb[i][2], hb[i][3]);
+  }
+  __syncthreads();  // the sum's reads of red are done before block_max writes it
+  const float scale = row_scale(block_max(amax, red));
+  if (threadIdx.x == 0) sx[m] = scale;
+  int8_t* out = xq + m * K;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
+    if (k >= K) continue;
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, hb[i][j] << 16), scale);
+      const uint32_t hi = (uint8_t)quant1(__builtin_bit_cast(float, hb[i][j] & 0xffff0000u), scale);
+      packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
+    }
+    *reinterpret_cast<uint2*>(out + k) = make_uint2(packed[0], packed[1]);
+  }
+}
+
 int launch_rmsnorm_quantize(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
                             int8_t* xq, float* sx, uint16_t* normed, int64_t M, int64_t K,
                             hipStream_t stream) {
-  hipLaunchKernelGGL(rmsnorm_quant_rows, dim3((unsigned)M), dim3(kQuantThreads), 0, stream, x, ldx,
-                     w, eps, xq, sx, normed, (int)K);
+  constexpr int64_t kRow = kQuantThreads * 8;  // elements per register slot of a row
+  const dim3 grid((unsigned)M), block(kQuantThreads);
+  if (K <= kRow)
+    hipLaunchKernelGGL(rmsnorm_quant_rows_reg<1>, grid, block, 0, stream, x, ldx, w, eps, xq, sx,
+                       normed, (int)K);
+  else if (K <= 2 * kRow)
+    hipLaunchKernelGGL(rmsnorm_quant_rows_reg<2>, grid, block, 0, stream, x, ldx, w, eps, xq, sx,
+                       normed, (int)K);
+  else if (K <= 4 * kRow)
+    hipLaunchKernelGGL(rmsnorm_quant_rows_reg<4>, grid, block, 0, stream, x, ldx, w, eps, xq, sx,
+                       normed, (int)K);
+  else
+    hipLaunchKernelGGL(rmsnorm_quant_rows, grid, block, 0, stream, x, ldx, w, eps, xq, sx, normed,
+                       (int)K);
   return launch_status();
 }
 

@@ -19,7 +19,8 @@ from oracle import numerics as ora
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("m,k", [(1, 4096), (37, 4096), (5, 2048), (64, 64), (3, 14336)])
+@pytest.mark.parametrize("m,k", [(1, 4096), (37, 4096), (5, 2048), (64, 64), (3, 14336), (9, 3072),
+                                 (4, 6144), (2, 8192), (2, 8208)])
 def test_matches_the_oracle(pkg, dev, m, k):
     rng = np.random.default_rng(m * 7 + k)
     x = rng.standard_normal((m, k), dtype=np.float32) * np.float32(2.0)
