@@ -95,3 +95,40 @@ def test_paged_attention_matches_the_torch_attention(runner, dev):
     rel = (got - ref).norm() / ref.norm()
     assert rel < 1e-2, f"relative logit difference {rel:.4f}"
     assert int((got.argmax(-1) == ref.argmax(-1)).sum()) >= 15
+
+
+def test_whole_step_replays_from_a_graph(runner, dev):
+    """The reference's graphed-decode invariant (tests/test_decode_graph.py:53-59: graphed ==
+    eager) on the swapped path: one whole decode step (embedding to logits) with the int8 linears
+    and the HIP paged attention, captured into a graph, equals the eager step bitwise on every
+    replay, with eager steps in between. Each step writes the same K/V values at the same
+    position, so every run sees the same state."""
+    if runner.int8 is None:
+        runner.quantize("int8")
+    runner.use("int8")
+    if runner.k_pool is None:
+        runner.enable_paged()
+    runner.use_attention("paged")
+    gen = torch.Generator().manual_seed(16)
+    tok = torch.randint(0, runner.model.config.vocab_size, (16,), generator=gen).to(dev)
+    pos = 37
+    eager = runner.step(tok, pos).clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        runner.step(tok, pos)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = runner.step(tok, pos)
+    try:
+        for i in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {i}"
+            again = runner.step(tok, pos)
+            torch.cuda.synchronize()
+            assert torch.equal(again, eager), f"eager after replay {i}"
+    finally:
+        runner.use_attention("torch")
