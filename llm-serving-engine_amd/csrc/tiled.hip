@@ -311,18 +311,21 @@ static const void* tiled_kernel_for(const TiledShape& sh) {
 // efficiency (big tiles need fewer LDS bytes per MFMA; small tiles fill the CUs when there are
 // few tiles). A 128 x 128 tile keeps two blocks per CU, so its efficiency is the one measured
 // with two resident. Efficiencies relative to 256 x 256, measured on MI355X at M = 8192 (many
-// rounds), per mode; this picks the fastest of the four tiles on each of the 18 Llama-3-8B
-// prefill shapes timed (qkv, o_proj, gate_up, down at M = 512 and 2048, gate_up at 8192; both
-// modes).
+// rounds), per mode, except the 64 x 128 tile's, fitted at M = 256..2048 where it competes. On
+// the Llama-3-8B prefill shapes timed (qkv, o_proj, gate_up, down at M = 256 to 2048, gate_up at
+// 8192) this picks the fastest tile, or one within 6 % (qkv at M = 512).
 template <bool I8>
 static TiledShape tiled_shape(int64_t M, int64_t N, int cus) {
-  static const TiledShape cand[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
-  static const double eff16[] = {1.0, 0.86, 0.87, 0.835};
+  // W8A16 also has a 64 x 128 tile (four waves; it fills the CUs when M is a few hundred and N
+  // is narrow, e.g. o_proj and down at M = 256..512, 22-25 % faster than 128 x 128 there).
+  static const TiledShape cand[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 128}};
+  static const double eff16[] = {1.0, 0.86, 0.87, 0.835, 0.6};
   static const double eff8[] = {1.0, 0.81, 0.865, 0.86};
   const double* eff = I8 ? eff8 : eff16;
+  const int ncand = I8 ? 4 : 5;
   TiledShape best = cand[0];
   double best_cost = 1e300;
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < ncand; ++i) {
     const int64_t blocks = ceil_div(M, cand[i].bm) * ceil_div(N, cand[i].bn);
     const double cost = (double)ceil_div(blocks, (int64_t)cus) * cand[i].bm * cand[i].bn / eff[i];
     if (cost < best_cost * 0.999) {
