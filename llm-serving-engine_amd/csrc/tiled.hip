@@ -295,11 +295,17 @@ static const void* tiled_fn() {
 template <bool I8, bool GLU>
 static const void* tiled_kernel_for(const TiledShape& sh) {
   if constexpr (!I8) {
-    // 17..64 tokens over a wide weight (launch_w8a16_wide_decode): four waves of BM x 32.
+    // 64 x 128 (narrow prefill; 33..64 tokens over a wide weight, launch_w8a16_wide_decode) and
+    // 32 x 128 (17..32 tokens over a wide weight): four waves of BM x 32.
     if (sh.bm == 64)
       return reinterpret_cast<const void*>(&tiled_gemm_kernel<false, 64, 128, 1, 4, 4, GLU>);
     if (sh.bm == 32)
       return reinterpret_cast<const void*>(&tiled_gemm_kernel<false, 32, 128, 1, 4, 4, GLU>);
+  } else {
+    // 64 x 128 for narrow W8A8 prefill: four waves of 32 x 64 (2 x 2 measured 1-8 % faster
+    // than 1 x 4 on MI355X).
+    if (sh.bm == 64)
+      return reinterpret_cast<const void*>(&tiled_gemm_kernel<true, 64, 128, 2, 2, 4, GLU>);
   }
   if (sh.bm == 256 && sh.bn == 256) return tiled_fn<I8, 256, 256, GLU>();
   if (sh.bm == 256 && sh.bn == 128) return tiled_fn<I8, 256, 128, GLU>();
@@ -316,16 +322,15 @@ static const void* tiled_kernel_for(const TiledShape& sh) {
 // 8192) this picks the fastest tile, or one within 6 % (qkv at M = 512).
 template <bool I8>
 static TiledShape tiled_shape(int64_t M, int64_t N, int cus) {
-  // W8A16 also has a 64 x 128 tile (four waves; it fills the CUs when M is a few hundred and N
-  // is narrow, e.g. o_proj and down at M = 256..512, 22-25 % faster than 128 x 128 there).
+  // The 64 x 128 tile (four waves) fills the CUs when M is a few hundred and N is narrow, e.g.
+  // o_proj and down at M = 256..512: 16-25 % faster than 128 x 128 there, in both modes.
   static const TiledShape cand[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 128}};
   static const double eff16[] = {1.0, 0.86, 0.87, 0.835, 0.6};
-  static const double eff8[] = {1.0, 0.81, 0.865, 0.86};
+  static const double eff8[] = {1.0, 0.81, 0.865, 0.86, 0.6};
   const double* eff = I8 ? eff8 : eff16;
-  const int ncand = I8 ? 4 : 5;
   TiledShape best = cand[0];
   double best_cost = 1e300;
-  for (int i = 0; i < ncand; ++i) {
+  for (int i = 0; i < 5; ++i) {
     const int64_t blocks = ceil_div(M, cand[i].bm) * ceil_div(N, cand[i].bn);
     const double cost = (double)ceil_div(blocks, (int64_t)cus) * cand[i].bm * cand[i].bn / eff[i];
     if (cost < best_cost * 0.999) {
