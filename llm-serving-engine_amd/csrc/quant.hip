@@ -54,7 +54,8 @@ quantize_weight_rows(const float* __restrict__ w, int64_t ldw, int8_t* __restric
   }
 }
 
-// One workgroup per token; bf16 input read twice (the second pass hits L2).
+// One workgroup per token; bf16 input read twice (the second pass hits L2). Rows longer than 8192
+// elements; shorter ones take quantize_act_rows_reg.
 __global__ void __launch_bounds__(kQuantThreads)
 quantize_act_rows(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ xq,
                   float* __restrict__ sx, int K) {
@@ -265,10 +266,59 @@ int launch_quantize_weight(const float* w, int64_t ldw, int8_t* q, float* s, int
   return launch_status();
 }
 
+// The same for rows of at most NV x 2048 elements: thread t keeps elements 8 t + 2048 i (i < NV)
+// in registers, so the row is read once. The row maximum is order-independent and each element's
+// quantization is the same expression, so the results are bit-identical to quantize_act_rows.
+template <int NV>
+__global__ void __launch_bounds__(kQuantThreads)
+quantize_act_rows_reg(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ xq,
+                      float* __restrict__ sx, int K) {
+  __shared__ float red[kQuantThreads / 64];
+  const int64_t m = blockIdx.x;
+  const uint16_t* row = x + m * ldx;
+  uint32_t u[NV][4];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
+    const uint4 v = k < K ? *reinterpret_cast<const uint4*>(row + k) : make_uint4(0, 0, 0, 0);
+    u[i][0] = v.x, u[i][1] = v.y, u[i][2] = v.z, u[i][3] = v.w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      amax = fmaxf(amax, fabsf(__builtin_bit_cast(float, u[i][j] << 16)));
+      amax = fmaxf(amax, fabsf(__builtin_bit_cast(float, u[i][j] & 0xffff0000u)));
+    }
+  }
+  const float scale = row_scale(block_max(amax, red));
+  if (threadIdx.x == 0) sx[m] = scale;
+  int8_t* out = xq + m * K;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
+    if (k >= K) continue;
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, u[i][j] << 16), scale);
+      const uint32_t hi = (uint8_t)quant1(__builtin_bit_cast(float, u[i][j] & 0xffff0000u), scale);
+      packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
+    }
+    *reinterpret_cast<uint2*>(out + k) = make_uint2(packed[0], packed[1]);
+  }
+}
+
 int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, int64_t M,
                         int64_t K, hipStream_t stream) {
-  hipLaunchKernelGGL(quantize_act_rows, dim3((unsigned)M), dim3(kQuantThreads), 0, stream, x, ldx,
-                     xq, sx, (int)K);
+  constexpr int64_t kRow = kQuantThreads * 8;  // elements per register slot of a row
+  const dim3 grid((unsigned)M), block(kQuantThreads);
+  if (K <= kRow)
+    hipLaunchKernelGGL(quantize_act_rows_reg<1>, grid, block, 0, stream, x, ldx, xq, sx, (int)K);
+  else if (K <= 2 * kRow)
+    hipLaunchKernelGGL(quantize_act_rows_reg<2>, grid, block, 0, stream, x, ldx, xq, sx, (int)K);
+  else if (K <= 4 * kRow)
+    hipLaunchKernelGGL(quantize_act_rows_reg<4>, grid, block, 0, stream, x, ldx, xq, sx, (int)K);
+  else
+    hipLaunchKernelGGL(quantize_act_rows, grid, block, 0, stream, x, ldx, xq, sx, (int)K);
   return launch_status();
 }
 

@@ -79,7 +79,8 @@ def _quant_act(pkg, dev, x_bits):
     return xq.cpu().numpy(), sx.cpu().numpy()
 
 
-@pytest.mark.parametrize("m,k", [(1, 16), (3, 48), (32, 4096), (512, 14336), (4096, 4096)])
+@pytest.mark.parametrize("m,k", [(1, 16), (3, 48), (32, 4096), (512, 14336), (4096, 4096),
+                                 (7, 3072), (5, 6144), (3, 8192), (2, 8208)])
 def test_act_quant_bit_exact_with_outliers(pkg, dev, m, k):
     """Config-3 activations: N(0,1) bf16 with round(0.001 K) columns scaled x20."""
     x_bits, _ = ora.seeded_inputs(3000 + m + k, m, 1, k, outliers=True)
