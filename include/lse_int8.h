@@ -76,7 +76,7 @@ enum lse_query_key {
   LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
 };
 
-#define LSE_ABI_VERSION 7
+#define LSE_ABI_VERSION 8
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -174,6 +174,22 @@ int lse_rmsnorm_quantize(const void* x, int64_t ldx, const void* weight, float e
 int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s, void* y,
                   int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* workspace,
                   int64_t workspace_bytes, void* stream);
+
+/*
+ * W8A8 linear from bf16 activations in one launch: y (and acc) exactly as
+ * lse_quantize_act_per_token followed by lse_w8a8_gemm compute them, bit for bit, with the
+ * per-token quantization done by the GEMM kernel itself (no xq / sx round trip, one launch).
+ * x: (M, K) bf16, row stride ldx (multiple of 8, 16-byte aligned base); the rest as for
+ * lse_w8a8_gemm. Needs no workspace. Runs when lse_w8a8_linear_supported(M, K) (small decode
+ * batches: M <= 16 and M * K int8 bytes fit the kernel's staged image); otherwise returns
+ * LSE_E_ALGO and the caller quantizes and calls lse_w8a8_gemm.
+ * Replaces: `F.linear(x, W)` (torch/nn/modules/linear.py:134) at the decode call sites of the
+ * dynamic per-token mode, where x arrives in bf16 (o_proj after attention, down_proj after the
+ * SiLU-mul; model_runner.py:369, modeling_llama.py:175).
+ */
+int lse_w8a8_linear_supported(int64_t M, int64_t K);
+int lse_w8a8_linear(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
+                    int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Bytes of the packed gate/up layout of two (I, K) weights: 2 * ceil(I/16) * ceil(K/64) * 1024. */
 int64_t lse_packed_glu_bytes(int64_t I, int64_t K);

@@ -28,6 +28,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lse_quantize_act_per_token": (_INT, [_P, _I64, _P, _P, _I64, _I64, _P]),
     "lse_rmsnorm_quantize": (_INT, [_P, _I64, _P, ctypes.c_float, _P, _P, _P, _I64, _I64, _P]),
     "lse_w8a8_gemm": (_INT, [_P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P]),
+    "lse_w8a8_linear_supported": (_INT, [_I64, _I64]),
+    "lse_w8a8_linear": (_INT, [_P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P]),
     "lse_packed_glu_bytes": (_I64, [_I64, _I64]),
     "lse_pack_glu": (_INT, [_P, _I64, _I64, _P, _P]),
     "lse_w8a16_glu": (_INT, [_P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]),
@@ -49,7 +51,7 @@ ALGO_AUTO, ALGO_DECODE, ALGO_PREFILL = 0, 1, 2
 MODE_W8A16, MODE_W8A8 = 0, 1
 E_WORKSPACE = -6
 Q_ABI_VERSION, Q_K_ALIGN, Q_DECODE_MAX_M, Q_MAX_K, Q_GFX_ARCH = 0, 1, 2, 3, 4
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -26,6 +26,10 @@ int launch_w8a16_skinny(const uint16_t* x, int64_t ldx, const int8_t* qp, const 
 int launch_w8a8_skinny(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
                        uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
                        void* ws, int64_t ws_bytes, hipStream_t stream);
+bool w8a8_quantizing_supported(int64_t M, int64_t K);
+int launch_w8a8_skinny_quantizing(const uint16_t* x, int64_t ldx, const int8_t* qp,
+                                  const float* s, uint16_t* y, int64_t ldy, int32_t* acc,
+                                  int64_t M, int64_t N, int64_t K, hipStream_t stream);
 int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* q, const float* s, uint16_t* y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s,
@@ -288,6 +292,25 @@ int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const flo
   }
   if (256 * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
   return lse::launch_w8a8_gemm(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, st);
+}
+
+int lse_w8a8_linear_supported(int64_t M, int64_t K) {
+  return K > 0 && K % LSE_K_ALIGN == 0 && K <= LSE_MAX_K && lse::w8a8_quantizing_supported(M, K);
+}
+
+int lse_w8a8_linear(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
+                    int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream) {
+  if (int st = check_common(qp, s, M, N, K)) return st;
+  if (M == 0 || N == 0) return LSE_OK;
+  if (!lse_w8a8_linear_supported(M, K)) return LSE_E_ALGO;
+  if (y) {
+    if (int st = check_bf16_matrix(y, ldy, M, N, 1)) return st;
+  }
+  if (acc && !aligned(acc, 16)) return LSE_E_ALIGN;
+  if (int e = check_bf16_matrix(x, ldx, M, K, 8)) return e;
+  if (int e = check_packed(N, K)) return e;
+  return lse::launch_w8a8_skinny_quantizing((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy,
+                                            acc, M, N, K, (hipStream_t)stream);
 }
 
 int lse_w8a16_glu(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* h,

@@ -220,6 +220,16 @@ __device__ __forceinline__ void dma16_lds_seq(u32x4 r, uint32_t base, const uint
 // so it is safe during stream capture.
 int persistent_blocks(const void* kernel, int threads, size_t dyn_lds = 0);
 
+// Per-token (and per-channel) symmetric int8 quantization, shared by the quantizers and the
+// decode kernel's quantizing staging: scale = fl32(amax / 127) (IEEE division; an all-zero row
+// gets 1), q = clamp(rne(fl32(v / scale)), -127, 127).
+__device__ __forceinline__ float row_scale(float amax) { return amax > 0.0f ? amax / 127.0f : 1.0f; }
+
+__device__ __forceinline__ int8_t quant1(float v, float scale) {
+  const float t = __builtin_rintf(v / scale);
+  return (int8_t)fminf(fmaxf(t, -127.0f), 127.0f);
+}
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LSE_OK : (int)e;

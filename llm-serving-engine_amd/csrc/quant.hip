@@ -22,12 +22,6 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return m;
 }
 
-__device__ __forceinline__ int8_t quant1(float v, float scale) {
-  const float t = __builtin_rintf(v / scale);
-  return (int8_t)fminf(fmaxf(t, -127.0f), 127.0f);
-}
-
-__device__ __forceinline__ float row_scale(float amax) { return amax > 0.0f ? amax / 127.0f : 1.0f; }
 
 // One workgroup per weight row; fp32 input read twice (the second pass hits L2).
 __global__ void __launch_bounds__(kQuantThreads)

@@ -104,11 +104,14 @@ __host__ __device__ constexpr int skinny_swz_mask(int chunks_per_row) {
   return ((chunks_per_row & -chunks_per_row) < 16 ? (chunks_per_row & -chunks_per_row) : 16) - 1;
 }
 
-template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU, bool BFW = false>
+template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU, bool BFW = false,
+          bool QX = false>
 __global__ void __launch_bounds__(64 * W)
 skinny_kernel(SkinnyArgs a) {
   using Acc = std::conditional_t<I8, i32x4, f32x4>;
   static_assert(!BFW || (!I8 && !GLU), "bf16 weights: plain W16A16 only");
+  // QX: x is bf16 and the kernel quantizes it per token while staging it (W8A8 in one launch).
+  static_assert(!QX || (I8 && XLDS && MT == 1 && !GLU && !BFW), "quantizing staging: W8A8, M <= 16");
   constexpr int WN = BFW ? 2 : 1;  // 1 KB weight tiles per row tile and step
   constexpr int SLICES = RT * MT;               // 16x16 output tiles of a panel
   constexpr int ESZ = I8 ? 1 : 2;               // activation element bytes
@@ -142,6 +145,7 @@ skinny_kernel(SkinnyArgs a) {
 
   __shared__ Acc red[W][RS][64];
   __shared__ float s_lds[kSkinnyScaleLds];
+  __shared__ unsigned qx_amax[QX ? 16 : 1];  // QX: each token row's max |x|, as float bits
   __shared__ uint4 xs0[XSLOT], xs1[DX > 1 ? XSLOT : 1], xs2[DX > 2 ? XSLOT : 1],
       xs3[DX > 3 ? XSLOT : 1];
   static_assert(XLDS || DX <= 4, "at most four activation slots");
@@ -171,7 +175,7 @@ skinny_kernel(SkinnyArgs a) {
 #pragma unroll
   for (int b = 0; b < MT; ++b) {
     const int m = 16 * b + r16;
-    sxv[b] = (I8 && m < a.M) ? a.sx[m] : 0.0f;
+    sxv[b] = (I8 && !QX && m < a.M) ? a.sx[m] : 0.0f;  // QX: set while staging
   }
 
   // Staged inputs, issued before the weight ring: with S = 1 (units are panels) the scales of
@@ -199,7 +203,7 @@ skinny_kernel(SkinnyArgs a) {
   }
   const int xrow_bytes = skinny_x_row(a.K, ESZ);
   const int xswz = skinny_swz_mask(xrow_bytes / 16);
-  if constexpr (XLDS) {
+  if constexpr (XLDS && !QX) {
     const int total = (a.M * xrow_bytes + 1023) / 1024;
     for (int piece = wave; piece < total; piece += W) {
       const int o = 1024 * piece + 16 * lane;
@@ -219,7 +223,54 @@ skinny_kernel(SkinnyArgs a) {
       const int r = threadIdx.x + 64 * W * i;
       if (r < kSkinnyScaleLds) s_lds[r] = sc_stage[i];
     }
-    if constexpr (XLDS) __builtin_amdgcn_s_waitcnt(vmcnt_imm((DW - 1) * RT * WN));
+    if constexpr (XLDS && !QX) __builtin_amdgcn_s_waitcnt(vmcnt_imm((DW - 1) * RT * WN));
+    if constexpr (QX) {
+      // Per-token quantization of the bf16 rows into the staged int8 image, bit for bit what
+      // quantize_act_rows computes: each row's max |x| (an LDS atomic max on the float bits,
+      // which order like the values since they are >= 0), then every element's quant1 with the
+      // row's scale, written at its swizzled position (chunk pc of row m holds logical chunk
+      // pc ^ (m & xswz); K is a multiple of 16, so a 16-element chunk is wholly in or out).
+      if (threadIdx.x < 16) qx_amax[threadIdx.x] = 0u;
+      __syncthreads();
+      const uint16_t* xb = static_cast<const uint16_t*>(a.x);
+      const int kch = a.K / 8;
+      for (int c = threadIdx.x; c < a.M * kch; c += 64 * W) {
+        const int m = c / kch, k8 = 8 * (c - m * kch);
+        const uint4 v = *reinterpret_cast<const uint4*>(xb + (int64_t)m * a.ldx + k8);
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          mx = fmaxf(mx, fabsf(__builtin_bit_cast(float, w4[j] << 16)));
+          mx = fmaxf(mx, fabsf(__builtin_bit_cast(float, w4[j] & 0xffff0000u)));
+        }
+        atomicMax(&qx_amax[m], __builtin_bit_cast(unsigned, mx));
+      }
+      __syncthreads();
+      const int rch = xrow_bytes / 16;  // 16-byte chunks per staged row
+      for (int c = threadIdx.x; c < a.M * rch; c += 64 * W) {
+        const int m = c / rch, pc = c - m * rch;
+        const int k16 = 16 * (pc ^ (m & xswz));
+        const float scale = row_scale(__builtin_bit_cast(float, qx_amax[m]));
+        uint32_t packed[4] = {0, 0, 0, 0};
+        if (k16 < a.K) {
+          const uint16_t* src = xb + (int64_t)m * a.ldx + k16;
+          const uint4 v0 = *reinterpret_cast<const uint4*>(src);
+          const uint4 v1 = *reinterpret_cast<const uint4*>(src + 8);
+          const uint32_t w8[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, w8[j] << 16), scale);
+            const uint32_t hi =
+                (uint8_t)quant1(__builtin_bit_cast(float, w8[j] & 0xffff0000u), scale);
+            packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
+          }
+        }
+        *reinterpret_cast<uint4*>(x_lds + 16 * c) = make_uint4(packed[0], packed[1], packed[2],
+                                                                packed[3]);
+      }
+      sxv[0] = r16 < a.M ? row_scale(__builtin_bit_cast(float, qx_amax[r16])) : 0.0f;
+    }
     __syncthreads();
   };
 
@@ -526,9 +577,9 @@ struct SkinnyShape {
 };
 
 template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU = false,
-          bool BFW = false>
+          bool BFW = false, bool QX = false>
 static const void* skinny_fn() {
-  return reinterpret_cast<const void*>(&skinny_kernel<I8, MT, RT, W, DW, DX, XLDS, GLU, BFW>);
+  return reinterpret_cast<const void*>(&skinny_kernel<I8, MT, RT, W, DW, DX, XLDS, GLU, BFW, QX>);
 }
 
 // Panel height for 17..64 tokens: each panel re-reads the activations from L2, so panels are as
@@ -723,6 +774,32 @@ int launch_w8a16_skinny_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, co
                             hipStream_t stream) {
   return skinny_run<false>(x, ldx, qp, s, nullptr, h, ldh, nullptr, M, 0, K, I, nullptr, 0,
                            stream);
+}
+
+// W8A8 from bf16 activations in one launch, for M <= 16 tokens whose int8 rows fit the staged
+// image: the decode kernel quantizes x per token while staging it (QX). Results are bit-identical
+// to lse_quantize_act_per_token followed by the decode kernel.
+bool w8a8_quantizing_supported(int64_t M, int64_t K) {
+  return M >= 1 && M <= 16 && M * (int64_t)skinny_x_row((int)K, 1) <= kSkinnyXLdsBytes;
+}
+
+int launch_w8a8_skinny_quantizing(const uint16_t* x, int64_t ldx, const int8_t* qp,
+                                  const float* s, uint16_t* y, int64_t ldy, int32_t* acc,
+                                  int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  const SkinnyShape sh = skinny_shape<true>(M, N, K);
+  if (sh.mt != 1 || !sh.xlds || sh.splits != 1) return LSE_E_ALGO;
+  SkinnyPlan pl = skinny_plan_for<true>(
+      sh, skinny_fn<true, 1, 1, 8, 4, 1, true, false, false, true>(), M, N, K);
+  SkinnyArgs& a = pl.a;
+  a.x = x;
+  a.ldx = ldx;
+  a.qp = qp;
+  a.s = s;
+  a.sx = nullptr;
+  a.y = y;
+  a.ldy = ldy;
+  a.acc = acc;
+  return skinny_launch<true>(pl, nullptr, stream);
 }
 
 int launch_w8a8_skinny_glu(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,

@@ -251,13 +251,37 @@ def w8a8_gemm(
     return y, acc
 
 
-def w8a8_linear(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+def w8a8_linear(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor,
+                want_acc: bool = False):
     """Dynamic per-token W8A8: quantize x per row, int8 GEMM with exact int32 accumulation,
-    y = bf16((acc * sx[m]) * s[n]). x (..., K) bf16 → y (..., N) bf16."""
-    n = scales.shape[0]
-    xq, sx = quantize_act_per_token(x)
-    y, _ = w8a8_gemm(xq, sx, qp, scales)
-    return y.view(*x.shape[:-1], n)
+    y = bf16((acc * sx[m]) * s[n]). x (..., K) bf16 → y (..., N) bf16 (with want_acc, also the
+    (M, N) int32 accumulators). Small decode batches run as one kernel that quantizes while it
+    stages x (`lse_w8a8_linear`); others quantize first, then run the GEMM. Both give the same
+    bits."""
+    n, k = scales.shape[0], x.shape[-1]
+    lib = _lib.library()
+    m = x.numel() // k if k else 0
+    if m and lib.lse_w8a8_linear_supported(m, k):
+        dev = _on_gpu(x, qp, scales)
+        _require(x.dtype == torch.bfloat16, f"W8A8 expects bf16 activations, got {x.dtype}")
+        _require(scales.dtype == torch.float32 and scales.dim() == 1, "scales must be fp32 (N,)")
+        _check_packed(qp, n, k)
+        x2 = _rows(x, k)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        acc = torch.empty((m, n), dtype=torch.int32, device=dev) if want_acc else None
+        ldx = x2.stride(0) if m > 1 else k
+        _lib.check(
+            lib.lse_w8a8_linear(
+                x2.data_ptr(), ldx, qp.data_ptr(), scales.data_ptr(), y.data_ptr(), n,
+                acc.data_ptr() if acc is not None else None, m, n, k, _stream(dev),
+            ),
+            "lse_w8a8_linear",
+        )
+    else:
+        xq, sx = quantize_act_per_token(x)
+        y, acc = w8a8_gemm(xq, sx, qp, scales, want_acc=want_acc)
+    y = y.view(*x.shape[:-1], n)
+    return (y, acc) if want_acc else y
 
 
 def w8a16_glu(

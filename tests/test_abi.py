@@ -149,6 +149,26 @@ def test_quantizers_and_w8a8_reject_bad_arguments(pkg):
     assert lib.lse_w8a8_gemm(None, FAKE, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, None, 0, None) == E_NULL
 
 
+def test_fused_w8a8_linear_eligibility_and_rejections(pkg):
+    """The one-launch W8A8 path runs for small decode batches whose int8 rows fit the staged
+    image (M <= 16, M * K <= 128 KB) and refuses everything else before any launch."""
+    lib = pkg.library()
+    assert lib.lse_w8a8_linear_supported(1, 4096) == 1
+    assert lib.lse_w8a8_linear_supported(16, 8192) == 1
+    assert lib.lse_w8a8_linear_supported(9, 14336) == 1   # 9 x 14336 bytes <= 128 KB
+    assert lib.lse_w8a8_linear_supported(10, 14336) == 0
+    assert lib.lse_w8a8_linear_supported(17, 4096) == 0
+    assert lib.lse_w8a8_linear_supported(0, 4096) == 0
+    assert lib.lse_w8a8_linear_supported(1, 40) == 0      # K not a multiple of 16
+    assert lib.lse_w8a8_linear(FAKE, 64, FAKE, FAKE, FAKE, 64, None, 17, 64, 64, None) == E_ALGO
+    assert lib.lse_w8a8_linear(FAKE, 64, FAKE, FAKE, FAKE, 64, None, -1, 64, 64, None) == E_SHAPE
+    assert lib.lse_w8a8_linear(FAKE, 64, None, FAKE, FAKE, 64, None, 2, 64, 64, None) == E_NULL
+    assert lib.lse_w8a8_linear(FAKE, 60, FAKE, FAKE, FAKE, 64, None, 2, 64, 64, None) == E_SHAPE
+    assert lib.lse_w8a8_linear(FAKE, 64, FAKE, FAKE, FAKE, 64, ctypes.c_void_p((1 << 20) + 4),
+                               2, 64, 64, None) == E_ALIGN
+    assert lib.lse_w8a8_linear(None, 0, FAKE, FAKE, None, 0, None, 0, 64, 64, None) == 0
+
+
 def test_status_strings(pkg):
     lib = pkg.library()
     for st in (0, E_NULL, E_SHAPE, E_ALIGN, E_RANGE, E_ALGO, E_WORKSPACE, -99):

@@ -109,3 +109,47 @@ def test_acc_only_and_y_only(pkg, dev):
     assert none_acc is None and none_y is None
     y_both, acc_both = pkg.ops.w8a8_gemm(xq, sx, qt, st, want_acc=True, want_y=True)
     assert torch.equal(acc_only, acc_both) and torch.equal(y_only, y_both)
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 16])
+@pytest.mark.parametrize("n,k", [(272, 1024), (100, 176), (48, 4096), (33, 2064)])
+def test_fused_linear_bit_exact(pkg, dev, m, n, k):
+    """W8A8 from bf16 in one launch (the decode kernel quantizes while staging): xq and sx never
+    leave the kernel, and acc and y equal the oracle's bit for bit, and the two-step path's."""
+    assert pkg.library().lse_w8a8_linear_supported(m, k)
+    x_bits, w = ora.seeded_inputs(900 + 7 * m + n + k, m, n, k, outliers=True)
+    if m > 2:
+        x_bits[2] = 0  # all-zero token: sx = 1, xq = 0
+    q, s = ora.quantize_weight_per_channel(w)
+    x = to_bf16_tensor(x_bits, dev)
+    qp = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
+    st = torch.from_numpy(s).to(dev)
+    y, acc = pkg.ops.w8a8_linear(x, qp, st, want_acc=True)
+    torch.cuda.synchronize()
+    xq_ref, sx_ref = ora.quantize_act_per_token(x_bits)
+    acc_ref = ora.w8a8_accumulate(xq_ref, q)
+    np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref, err_msg=f"acc M={m} N={n} K={k}")
+    np.testing.assert_array_equal(bf16_bits(y), ora.w8a8_epilogue(acc_ref, sx_ref, s))
+    _, _, acc2, y2 = _w8a8(pkg, dev, x_bits, q, s)
+    np.testing.assert_array_equal(acc.cpu().numpy(), acc2)
+    np.testing.assert_array_equal(bf16_bits(y), y2)
+
+
+def test_fused_linear_deep_k_and_strided_rows(pkg, dev):
+    """The down projection's K (14336) at the largest M the staged image holds (9), and x rows
+    with a stride past K."""
+    m, n, k = 9, 64, 14336
+    assert pkg.library().lse_w8a8_linear_supported(m, k)
+    assert not pkg.library().lse_w8a8_linear_supported(m + 1, k)
+    x_bits, w = ora.seeded_inputs(977, m, n, k, outliers=True)
+    q, s = ora.quantize_weight_per_channel(w)
+    wide = np.zeros((m, k + 64), np.uint16)
+    wide[:, :k] = x_bits
+    x = to_bf16_tensor(wide, dev)[:, :k]
+    qp = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
+    y, acc = pkg.ops.w8a8_linear(x, qp, torch.from_numpy(s).to(dev), want_acc=True)
+    torch.cuda.synchronize()
+    xq_ref, sx_ref = ora.quantize_act_per_token(x_bits)
+    acc_ref = ora.w8a8_accumulate(xq_ref, q)
+    np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref)
+    np.testing.assert_array_equal(bf16_bits(y), ora.w8a8_epilogue(acc_ref, sx_ref, s))
