@@ -27,7 +27,9 @@
 //    h = bf16(silu(g) * u) for its I output columns. No K splits.
 //  * W8A16 with 17..64 tokens over a wide weight (at least 1024 row tiles, the MLP gate/up) does
 //    not run here: the decode dispatch sends it to a 32 x 128 or 64 x 128 tile of the tiled
-//    kernel (skinny_wide_tiled).
+//    kernel (skinny_wide_tiled); nor over a deep, narrow one (the split-K class, down_proj),
+//    which runs as 8 K ranges of such tiles whose partials skinny_reduce adds
+//    (skinny_deep_tiled).
 //  * bf16 weights (BFW, the lm_head kept in bf16): each 64-wide K step of a row tile is two
 //    1 KB tiles already in bf16 operand form (the "lo" and "hi" halves that dequantization
 //    produces from an int8 tile, layout in lse_common.h), loaded instead of dequantized; no
@@ -713,7 +715,40 @@ static int skinny_launch(SkinnyPlan& pl, void* part, hipStream_t stream) {
   return e == hipSuccess ? launch_status() : (int)e;
 }
 
+int64_t w8a16_deep_decode_part_bytes(int64_t M, int64_t N);  // tiled.hip
+int launch_w8a16_deep_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                             uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                             int64_t ws_bytes, hipStream_t stream);  // tiled.hip
+
+// W8A16 with 17..64 tokens over a deep, narrow weight (this kernel's split-K class: the MLP down
+// projection): 8 K ranges of 32 x 128 or 64 x 128 tiles of the tiled kernel, whose partial sums
+// skinny_reduce adds. Chosen by the token class, N and K only.
+static bool skinny_deep_tiled(int64_t M, int64_t N, int64_t K) {
+  return M > 16 && skinny_split_k(N, K);
+}
+
+// The second pass for the tiled kernel's split partial sums (the same [S][M][16 nrb] layout).
+int launch_skinny_reduce_w8a16(const float* part, const float* s, uint16_t* y, int64_t ldy,
+                               int64_t M, int64_t N, int splits, hipStream_t stream) {
+  SkinnyArgs a{};
+  a.M = (int)M;
+  a.N = (int)N;
+  a.nrb = (int)ceil_div(N, kTileRows);
+  a.splits = splits;
+  a.part = const_cast<float*>(part);
+  a.s = s;
+  a.y = y;
+  a.ldy = ldy;
+  void* args[] = {&a};
+  const int64_t threads = M * 4 * a.nrb;
+  const hipError_t e =
+      hipLaunchKernel(reinterpret_cast<const void*>(&skinny_reduce<false>),
+                      dim3((unsigned)ceil_div(threads, 256)), dim3(256), args, 0, stream);
+  return e == hipSuccess ? launch_status() : (int)e;
+}
+
 int64_t skinny_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K) {
+  if (!i8 && skinny_deep_tiled(M, N, K)) return w8a16_deep_decode_part_bytes(M, N);
   return i8 ? skinny_plan<true>(M, N, K).part_bytes : skinny_plan<false>(M, N, K).part_bytes;
 }
 
@@ -741,6 +776,9 @@ static int skinny_run(const void* x, int64_t ldx, const int8_t* qp, const float*
     if (!bfw && skinny_wide_tiled(M, rows))
       return launch_w8a16_wide_decode(static_cast<const uint16_t*>(x), ldx, qp, s, y, ldy, M, N,
                                       K, glu, stream);
+    if (!bfw && glu == 0 && skinny_deep_tiled(M, N, K))
+      return launch_w8a16_deep_decode(static_cast<const uint16_t*>(x), ldx, qp, s, y, ldy, M, N,
+                                      K, ws, ws_bytes, stream);
   }
   SkinnyPlan pl = skinny_plan<I8>(M, N, K, glu, bfw);
   if (ws_bytes < pl.part_bytes || (pl.part_bytes && !ws)) return LSE_E_WORKSPACE;

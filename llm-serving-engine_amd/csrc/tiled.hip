@@ -58,6 +58,9 @@ struct TiledArgs {
   int nrb;           // ceil(N / 16)
   int mblocks, nblocks;
   int glu;           // gate/up layout: I, the output columns (N = 16 nrb packed rows); else 0
+  int splits;        // > 1 (W8A16, no gate/up): K split into ranges of ssteps steps, raw fp32
+  int ssteps;        //   partial sums to part, added by the decode kernel's second pass
+  float* part;       // [splits][M][16 nrb]
 };
 
 constexpr int kGroupM = 4;
@@ -114,8 +117,13 @@ tiled_gemm_kernel(TiledArgs a) {
 
   // XCD-aware tile order (see the header comment): XCD x = b % 8 receives blocks x, x + 8, ...;
   // give it the contiguous tile range starting at the tiles of XCDs before it.
+  // K range of this block: all of K, or with splits > 1 its split's steps (blockIdx % splits).
+  const int S = a.splits > 1 ? a.splits : 1;
+  const int sp = blockIdx.x % S;
+  const int kbeg = sp * (S > 1 ? a.ssteps : 0);
+  const int kend = S > 1 ? min(kbeg + a.ssteps, a.nsteps) : a.nsteps;
   const int T = a.mblocks * a.nblocks;
-  const int b = blockIdx.x, xcd = b & 7, l = b >> 3, q8 = T >> 3, rem = T & 7;
+  const int b = blockIdx.x / S, xcd = b & 7, l = b >> 3, q8 = T >> 3, rem = T & 7;
   const int t = xcd * q8 + min(xcd, rem) + l;
   const int group = t / (kGroupM * a.nblocks), first_bm = group * kGroupM;
   const int gm = min(a.mblocks - first_bm, kGroupM);
@@ -150,14 +158,15 @@ tiled_gemm_kernel(TiledArgs a) {
     w_lds[i] = lds_addr(wslot(i) + 64 * wave);
   }
   auto load_stage = [&](int kt, int slot) {
-    const bool kv = kt < a.nsteps && XROW * kt + x_kb < a.K * ESZ;
+    kt += kbeg;  // stage index within the block's K range -> K step
+    const bool kv = kt < kend && XROW * kt + x_kb < a.K * ESZ;
     uint32_t xo[XI], wo[WI];
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
       const bool rv = x_r0 + W * RPL * i < rows;
       xo[i] = kv && rv ? x_base + (uint32_t)(i * x_step) + XROW * kt : kOutOfRange;
     }
-    const bool live = kt < a.nsteps;
+    const bool live = kt < kend;
 #pragma unroll
     for (int i = 0; i < WI; ++i) {
       const int tile = wave + W * i;
@@ -211,7 +220,8 @@ tiled_gemm_kernel(TiledArgs a) {
   // Prologue: stages 0 .. NST-2 in flight.
 #pragma unroll
   for (int i = 0; i < NST - 1; ++i) load_stage(i, i);
-  for (int kt0 = 0; kt0 < a.nsteps; kt0 += NST) {
+  const int nloc = kend - kbeg;  // K steps of this block
+  for (int kt0 = 0; kt0 < nloc; kt0 += NST) {
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
       const int kt = kt0 + i;
@@ -220,7 +230,7 @@ tiled_gemm_kernel(TiledArgs a) {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
       __builtin_amdgcn_s_barrier();
       load_stage(kt + NST - 1, (i + NST - 1) % NST);
-      if (kt < a.nsteps) compute(i);
+      if (kt < nloc) compute(i);
     }
   }
 
@@ -228,6 +238,23 @@ tiled_gemm_kernel(TiledArgs a) {
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // Epilogue. D tile (i, j): lane holds weight rows 4 g + r (r = 0..3) of token r16.
+  if constexpr (!I8 && !GLU) {
+    if (S > 1) {  // raw partial sums of split sp, rows padded to 16 nrb (whole f32x4 stores)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + wm * WM + 16 * i + r16;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = n0 + wn * WN + 16 * j + 4 * g;
+          if (n < 16 * a.nrb)
+            *reinterpret_cast<Acc*>(a.part + ((int64_t)sp * a.M + m) * (16 * a.nrb) + n) =
+                acc[i][j];
+        }
+      }
+      return;
+    }
+  }
   const bool yvec = a.y && (a.ldy & 3) == 0 && ((uintptr_t)a.y & 7) == 0;
   if constexpr (GLU) {
     // Row tile rb = rb0 + wn TN + j (even j: gate) covers output columns 16 (rb / 2) + 4 g + r.
@@ -407,6 +434,53 @@ int launch_w8a16_wide_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, c
                              int64_t glu, hipStream_t stream) {
   return launch_tiled<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, glu > 0 ? 0 : N, K, glu,
                              stream, true);
+}
+
+int launch_skinny_reduce_w8a16(const float* part, const float* s, uint16_t* y, int64_t ldy,
+                               int64_t M, int64_t N, int splits, hipStream_t stream);  // skinny.hip
+
+// The decode kernel's deep, narrow W8A16 class at 17..64 tokens (at most 256 row tiles and at
+// least 128 K steps: the MLP down projection; chosen by the decode dispatch). A 32 x 128 or
+// 64 x 128 tile over one of 8 K ranges per block fills the CUs (8 x 32 blocks for down_proj)
+// without the decode kernel's cross-wave reduction; the raw partial sums are added in split
+// order by the decode kernel's second pass. On MI355X down_proj (K 14336, N 4096) takes 18.6 us
+// against 20.1 us at 32 tokens and 22.1 us against 24.5 us at 64.
+constexpr int kDeepSplits = 8;
+
+int64_t w8a16_deep_decode_part_bytes(int64_t M, int64_t N) {
+  return (int64_t)kDeepSplits * M * kTileRows * ceil_div(N, kTileRows) * 4;
+}
+
+int launch_w8a16_deep_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                             uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                             int64_t ws_bytes, hipStream_t stream) {
+  if (!ws || ws_bytes < w8a16_deep_decode_part_bytes(M, N)) return LSE_E_WORKSPACE;
+  const TiledShape sh{M > 32 ? 64 : 32, 128};
+  TiledArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.qp = qp;
+  a.s = s;
+  a.y = y;
+  a.ldy = ldy;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.nsteps = (int)ceil_div(K, kTileK);
+  a.nrb = (int)ceil_div(N, kTileRows);
+  a.mblocks = (int)ceil_div(M, sh.bm);
+  a.nblocks = (int)ceil_div(N, sh.bn);
+  a.splits = kDeepSplits;
+  a.ssteps = (int)ceil_div(a.nsteps, kDeepSplits);
+  a.part = static_cast<float*>(ws);
+  void* args[] = {&a};
+  const hipError_t e =
+      hipLaunchKernel(tiled_kernel_for<false, false>(sh),
+                      dim3((unsigned)(a.mblocks * a.nblocks * kDeepSplits)), dim3(256), args, 0,
+                      stream);
+  if (e != hipSuccess) return (int)e;
+  if (int st = launch_status()) return st;
+  return launch_skinny_reduce_w8a16(a.part, s, y, ldy, M, N, kDeepSplits, stream);
 }
 
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
