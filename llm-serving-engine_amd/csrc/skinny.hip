@@ -25,11 +25,10 @@
 //    even number of row tiles, so every panel holds matching gate and up rows; the final
 //    reduction adds slice pairs (gate tile, up tile) in one wave, which writes
 //    h = bf16(silu(g) * u) for its I output columns. No K splits.
-//  * W8A16 with 17..64 tokens over a wide weight (at least 1024 row tiles, the MLP gate/up) does
-//    not run here: the decode dispatch sends it to a 32 x 128 or 64 x 128 tile of the tiled
-//    kernel (skinny_wide_tiled); nor over a deep, narrow one (the split-K class, down_proj),
-//    which runs as 8 K ranges of such tiles whose partials skinny_reduce adds
-//    (skinny_deep_tiled).
+//  * 17..64 tokens over a wide weight (at least 1024 row tiles, the MLP gate/up) do not run here:
+//    the decode dispatch sends them to 32 x 128 or 64 x 128 tiles of the tiled kernel
+//    (skinny_wide_tiled); nor over a deep, narrow one (the split-K class, down_proj), which runs
+//    as 8 K ranges of such tiles whose partials skinny_reduce adds (skinny_deep_tiled).
 //  * bf16 weights (BFW, the lm_head kept in bf16): each 64-wide K step of a row tile is two
 //    1 KB tiles already in bf16 operand form (the "lo" and "hi" halves that dequantization
 //    produces from an int8 tile, layout in lse_common.h), loaded instead of dequantized; no
@@ -715,40 +714,51 @@ static int skinny_launch(SkinnyPlan& pl, void* part, hipStream_t stream) {
   return e == hipSuccess ? launch_status() : (int)e;
 }
 
-int64_t w8a16_deep_decode_part_bytes(int64_t M, int64_t N);  // tiled.hip
+int64_t deep_decode_part_bytes(int64_t M, int64_t N);  // tiled.hip
 int launch_w8a16_deep_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
                              uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
                              int64_t ws_bytes, hipStream_t stream);  // tiled.hip
+int launch_w8a8_deep_decode(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                            uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N,
+                            int64_t K, void* ws, int64_t ws_bytes, hipStream_t stream);  // tiled.hip
+int launch_w8a8_wide_decode(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                            uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N,
+                            int64_t K, int64_t glu, hipStream_t stream);  // tiled.hip
 
-// W8A16 with 17..64 tokens over a deep, narrow weight (this kernel's split-K class: the MLP down
-// projection): 8 K ranges of 32 x 128 or 64 x 128 tiles of the tiled kernel, whose partial sums
-// skinny_reduce adds. Chosen by the token class, N and K only.
+// 17..64 tokens over a deep, narrow weight (this kernel's split-K class: the MLP down
+// projection): 8 K ranges of tiles of the tiled kernel, whose partial sums skinny_reduce adds.
+// Chosen by the token class, N and K only, in both modes.
 static bool skinny_deep_tiled(int64_t M, int64_t N, int64_t K) {
   return M > 16 && skinny_split_k(N, K);
 }
 
-// The second pass for the tiled kernel's split partial sums (the same [S][M][16 nrb] layout).
-int launch_skinny_reduce_w8a16(const float* part, const float* s, uint16_t* y, int64_t ldy,
-                               int64_t M, int64_t N, int splits, hipStream_t stream) {
+// The second pass for the tiled kernel's split partial sums (the same [S][M][16 nrb] layout):
+// fp32 partials and y in W8A16, int32 partials, y and acc in W8A8.
+int launch_skinny_reduce_parts(bool i8, const void* part, const float* s, const float* sx,
+                               uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N,
+                               int splits, hipStream_t stream) {
   SkinnyArgs a{};
   a.M = (int)M;
   a.N = (int)N;
   a.nrb = (int)ceil_div(N, kTileRows);
   a.splits = splits;
-  a.part = const_cast<float*>(part);
+  a.part = const_cast<void*>(part);
   a.s = s;
+  a.sx = sx;
   a.y = y;
   a.ldy = ldy;
+  a.acc = acc;
   void* args[] = {&a};
   const int64_t threads = M * 4 * a.nrb;
+  const void* fn = i8 ? reinterpret_cast<const void*>(&skinny_reduce<true>)
+                      : reinterpret_cast<const void*>(&skinny_reduce<false>);
   const hipError_t e =
-      hipLaunchKernel(reinterpret_cast<const void*>(&skinny_reduce<false>),
-                      dim3((unsigned)ceil_div(threads, 256)), dim3(256), args, 0, stream);
+      hipLaunchKernel(fn, dim3((unsigned)ceil_div(threads, 256)), dim3(256), args, 0, stream);
   return e == hipSuccess ? launch_status() : (int)e;
 }
 
 int64_t skinny_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K) {
-  if (!i8 && skinny_deep_tiled(M, N, K)) return w8a16_deep_decode_part_bytes(M, N);
+  if (skinny_deep_tiled(M, N, K)) return deep_decode_part_bytes(M, N);
   return i8 ? skinny_plan<true>(M, N, K).part_bytes : skinny_plan<false>(M, N, K).part_bytes;
 }
 
@@ -756,8 +766,8 @@ int launch_w8a16_wide_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, c
                              uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                              int64_t glu, hipStream_t stream);  // tiled.hip
 
-// W8A16 with 17..64 tokens over a wide weight (64-row panels in this kernel, never split): a
-// 32 x 128 or 64 x 128 tile of the tiled kernel instead. Here this kernel's waves split each
+// 17..64 tokens over a wide weight (64-row panels in this kernel, never split): a 32 x 128 or
+// 64 x 128 tile of the tiled kernel instead (64 x 128 in W8A8). Here this kernel's waves split each
 // panel's K steps and then add 8 or 16 partial tiles each through LDS; with 17 or more tokens
 // that reduction and the per-wave activation rings cost more than they save, while a tile over
 // the whole K shares one activation stage among its waves. Chosen by the token class and N only,
@@ -771,14 +781,20 @@ static int skinny_run(const void* x, int64_t ldx, const int8_t* qp, const float*
                       const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
                       int64_t N, int64_t K, int64_t glu, void* ws, int64_t ws_bytes,
                       hipStream_t stream, bool bfw = false) {
+  const int64_t rows = glu > 0 ? 2 * kTileRows * ceil_div(glu, kTileRows) : N;
   if constexpr (!I8) {
-    const int64_t rows = glu > 0 ? 2 * kTileRows * ceil_div(glu, kTileRows) : N;
     if (!bfw && skinny_wide_tiled(M, rows))
       return launch_w8a16_wide_decode(static_cast<const uint16_t*>(x), ldx, qp, s, y, ldy, M, N,
                                       K, glu, stream);
     if (!bfw && glu == 0 && skinny_deep_tiled(M, N, K))
       return launch_w8a16_deep_decode(static_cast<const uint16_t*>(x), ldx, qp, s, y, ldy, M, N,
                                       K, ws, ws_bytes, stream);
+  } else {
+    const int8_t* xq = static_cast<const int8_t*>(x);
+    if (skinny_wide_tiled(M, rows))
+      return launch_w8a8_wide_decode(xq, sx, qp, s, y, ldy, acc, M, N, K, glu, stream);
+    if (glu == 0 && skinny_deep_tiled(M, N, K))
+      return launch_w8a8_deep_decode(xq, sx, qp, s, y, ldy, acc, M, N, K, ws, ws_bytes, stream);
   }
   SkinnyPlan pl = skinny_plan<I8>(M, N, K, glu, bfw);
   if (ws_bytes < pl.part_bytes || (pl.part_bytes && !ws)) return LSE_E_WORKSPACE;

@@ -58,9 +58,9 @@ struct TiledArgs {
   int nrb;           // ceil(N / 16)
   int mblocks, nblocks;
   int glu;           // gate/up layout: I, the output columns (N = 16 nrb packed rows); else 0
-  int splits;        // > 1 (W8A16, no gate/up): K split into ranges of ssteps steps, raw fp32
-  int ssteps;        //   partial sums to part, added by the decode kernel's second pass
-  float* part;       // [splits][M][16 nrb]
+  int splits;        // > 1 (no gate/up): K split into ranges of ssteps steps, raw partial sums
+  int ssteps;        //   (fp32, or int32 in W8A8) to part, added by the decode kernel's second
+  void* part;        //   pass; [splits][M][16 nrb]
 };
 
 constexpr int kGroupM = 4;
@@ -238,8 +238,9 @@ tiled_gemm_kernel(TiledArgs a) {
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // Epilogue. D tile (i, j): lane holds weight rows 4 g + r (r = 0..3) of token r16.
-  if constexpr (!I8 && !GLU) {
-    if (S > 1) {  // raw partial sums of split sp, rows padded to 16 nrb (whole f32x4 stores)
+  if constexpr (!GLU) {
+    if (S > 1) {  // raw partial sums of split sp, rows padded to 16 nrb (whole 16-byte stores)
+      Acc* part = static_cast<Acc*>(a.part);
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int m = m0 + wm * WM + 16 * i + r16;
@@ -247,9 +248,7 @@ tiled_gemm_kernel(TiledArgs a) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int n = n0 + wn * WN + 16 * j + 4 * g;
-          if (n < 16 * a.nrb)
-            *reinterpret_cast<Acc*>(a.part + ((int64_t)sp * a.M + m) * (16 * a.nrb) + n) =
-                acc[i][j];
+          if (n < 16 * a.nrb) part[(((int64_t)sp * a.M + m) * (16 * a.nrb) + n) / 4] = acc[i][j];
         }
       }
       return;
@@ -387,7 +386,7 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
                         int64_t N, int64_t K, int64_t glu, hipStream_t stream,
                         bool wide_decode = false) {
   if (glu > 0) N = 2 * kTileRows * ceil_div(glu, kTileRows);
-  const TiledShape sh = wide_decode ? TiledShape{M > 32 ? 64 : 32, 128}
+  const TiledShape sh = wide_decode ? TiledShape{(I8 || M > 32) ? 64 : 32, 128}
                                     : tiled_shape<I8>(M, N, device_cus());
   const int threads = sh.bm <= 64 ? 256 : kTiledThreads;
   TiledArgs a{};
@@ -436,33 +435,39 @@ int launch_w8a16_wide_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, c
                              stream, true);
 }
 
-int launch_skinny_reduce_w8a16(const float* part, const float* s, uint16_t* y, int64_t ldy,
-                               int64_t M, int64_t N, int splits, hipStream_t stream);  // skinny.hip
+int launch_skinny_reduce_parts(bool i8, const void* part, const float* s, const float* sx,
+                               uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N,
+                               int splits, hipStream_t stream);  // skinny.hip
 
-// The decode kernel's deep, narrow W8A16 class at 17..64 tokens (at most 256 row tiles and at
-// least 128 K steps: the MLP down projection; chosen by the decode dispatch). A 32 x 128 or
-// 64 x 128 tile over one of 8 K ranges per block fills the CUs (8 x 32 blocks for down_proj)
-// without the decode kernel's cross-wave reduction; the raw partial sums are added in split
-// order by the decode kernel's second pass. On MI355X down_proj (K 14336, N 4096) takes 18.6 us
-// against 20.1 us at 32 tokens and 22.1 us against 24.5 us at 64.
+// The decode kernel's deep, narrow class at 17..64 tokens (at most 256 row tiles and at least 128
+// K steps: the MLP down projection; chosen by the decode dispatch). Tiles of the tiled kernel
+// over one of 8 K ranges per block fill the CUs (8 x 32 blocks for down_proj) without the decode
+// kernel's cross-wave reduction; the raw partial sums are added in split order by the decode
+// kernel's second pass. W8A16: 32 x 128 or 64 x 128 tiles (class 17..32 or 33..64); on MI355X
+// down_proj (K 14336, N 4096) takes 18.7 us against 21.3 us at 32 tokens and 21.5 us against
+// 25.7 us at 64. W8A8: 64 x 128 tiles (int32 partials: exact, any order).
 constexpr int kDeepSplits = 8;
 
-int64_t w8a16_deep_decode_part_bytes(int64_t M, int64_t N) {
+int64_t deep_decode_part_bytes(int64_t M, int64_t N) {
   return (int64_t)kDeepSplits * M * kTileRows * ceil_div(N, kTileRows) * 4;
 }
 
-int launch_w8a16_deep_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
-                             uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
-                             int64_t ws_bytes, hipStream_t stream) {
-  if (!ws || ws_bytes < w8a16_deep_decode_part_bytes(M, N)) return LSE_E_WORKSPACE;
-  const TiledShape sh{M > 32 ? 64 : 32, 128};
+template <bool I8>
+static int launch_deep_decode(const void* x, int64_t ldx, const int8_t* qp, const float* s,
+                              const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
+                              int64_t N, int64_t K, void* ws, int64_t ws_bytes,
+                              hipStream_t stream) {
+  if (!ws || ws_bytes < deep_decode_part_bytes(M, N)) return LSE_E_WORKSPACE;
+  const TiledShape sh{(I8 || M > 32) ? 64 : 32, 128};
   TiledArgs a{};
   a.x = x;
   a.ldx = ldx;
   a.qp = qp;
   a.s = s;
+  a.sx = sx;
   a.y = y;
   a.ldy = ldy;
+  a.acc = acc;
   a.M = (int)M;
   a.N = (int)N;
   a.K = (int)K;
@@ -472,15 +477,37 @@ int launch_w8a16_deep_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, c
   a.nblocks = (int)ceil_div(N, sh.bn);
   a.splits = kDeepSplits;
   a.ssteps = (int)ceil_div(a.nsteps, kDeepSplits);
-  a.part = static_cast<float*>(ws);
+  a.part = ws;
   void* args[] = {&a};
   const hipError_t e =
-      hipLaunchKernel(tiled_kernel_for<false, false>(sh),
+      hipLaunchKernel(tiled_kernel_for<I8, false>(sh),
                       dim3((unsigned)(a.mblocks * a.nblocks * kDeepSplits)), dim3(256), args, 0,
                       stream);
   if (e != hipSuccess) return (int)e;
   if (int st = launch_status()) return st;
-  return launch_skinny_reduce_w8a16(a.part, s, y, ldy, M, N, kDeepSplits, stream);
+  return launch_skinny_reduce_parts(I8, ws, s, sx, y, ldy, acc, M, N, kDeepSplits, stream);
+}
+
+int launch_w8a16_deep_decode(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                             uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                             int64_t ws_bytes, hipStream_t stream) {
+  return launch_deep_decode<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, ws,
+                                   ws_bytes, stream);
+}
+
+int launch_w8a8_deep_decode(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                            uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N,
+                            int64_t K, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  return launch_deep_decode<true>(xq, K, qp, s, sx, y, ldy, acc, M, N, K, ws, ws_bytes, stream);
+}
+
+// W8A8 counterpart of launch_w8a16_wide_decode (17..64 tokens over a wide weight, plain or
+// gate/up): 64 x 128 int8 tiles over the whole K.
+int launch_w8a8_wide_decode(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
+                            uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N,
+                            int64_t K, int64_t glu, hipStream_t stream) {
+  return launch_tiled<true>(xq, K, qp, s, sx, y, ldy, acc, M, glu > 0 ? 0 : N, K, glu, stream,
+                            true);
 }
 
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,

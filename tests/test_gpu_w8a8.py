@@ -153,3 +153,10 @@ def test_fused_linear_deep_k_and_strided_rows(pkg, dev):
     acc_ref = ora.w8a8_accumulate(xq_ref, q)
     np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref)
     np.testing.assert_array_equal(bf16_bits(y), ora.w8a8_epilogue(acc_ref, sx_ref, s))
+
+
+@pytest.mark.parametrize("m", [20, 40])
+def test_wide_weight_tiles_bit_exact(pkg, dev, m):
+    """17..64 tokens over a weight of more than 1024 row tiles take 64 x 128 tiles of the tiled
+    kernel: accumulators and outputs stay bit-exact, with a partial last tile and a K tail."""
+    _check(pkg, dev, m, 16408, 80, 4100 + m)
