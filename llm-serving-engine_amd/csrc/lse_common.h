@@ -67,9 +67,16 @@ __device__ __forceinline__ BufferRsrc make_rsrc(const void* base, uint32_t bytes
                                            0x00020000);
 }
 
+// Cache policy of a buffer load (the instruction's cache-policy bits): kLoadDefault, or
+// kLoadStream (nt) for data read once per call, such as decode weights, so the stream does not
+// claim cache lines that reused data (activations, scales) need.
+constexpr int kLoadDefault = 0;
+constexpr int kLoadStream = 2;
+
+template <int POLICY = kLoadDefault>
 __device__ __forceinline__ uint4 buffer_load16(BufferRsrc r, uint32_t byte_offset) {
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0);
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, POLICY);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
@@ -193,25 +200,37 @@ __device__ __forceinline__ uint32_t lds_addr(const void* lds) {
       (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)lds);
 }
 
-// One load to LDS byte address base + IMM (+ 16 l for lane l).
-template <int IMM>
+// One load to LDS byte address base + IMM (+ 16 l for lane l); NT: the streaming (nt) cache
+// policy, for data read once per call.
+template <int IMM, bool NT = false>
 __device__ __forceinline__ void dma16_lds(u32x4 r, uint32_t base, uint32_t offset) {
   uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_add_u32 m0, %1, %4\n\t"
-      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(base), "v"(offset), "s"(r), "i"(IMM)
-      : "memory", "scc");
+  if constexpr (NT) {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_add_u32 m0, %1, %4\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(offset), "s"(r), "i"(IMM)
+        : "memory", "scc");
+  } else {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_add_u32 m0, %1, %4\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(offset), "s"(r), "i"(IMM)
+        : "memory", "scc");
+  }
 }
 
 // N loads, load i to base + i * STEP, from offsets off[i].
-template <int STEP, int... I>
+template <int STEP, bool NT = false, int... I>
 __device__ __forceinline__ void dma16_lds_seq(u32x4 r, uint32_t base, const uint32_t* off,
                                               std::integer_sequence<int, I...>) {
-  (dma16_lds<I * STEP>(r, base, off[I]), ...);
+  (dma16_lds<I * STEP, NT>(r, base, off[I]), ...);
 }
 
 // Workgroups of `kernel` (launched with `threads` threads and `dyn_lds` bytes of dynamic LDS)

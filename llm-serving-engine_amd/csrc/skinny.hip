@@ -288,7 +288,8 @@ skinny_kernel(SkinnyArgs a) {
           ((uint32_t)rb * (uint32_t)a.nsteps + (uint32_t)j) * (kTileBytes * WN) + 16u * lane;
 #pragma unroll
       for (int h = 0; h < WN; ++h)
-        st.w[WN * rt + h] = buffer_load16(qres, kv && rb < a.nrb ? off + kTileBytes * h : kOutOfRange);
+        st.w[WN * rt + h] =
+            buffer_load16<kLoadStream>(qres, kv && rb < a.nrb ? off + kTileBytes * h : kOutOfRange);
     }
     if (++lsu == a.NSU) {
       lsu = 0;
