@@ -81,7 +81,9 @@ __device__ __forceinline__ int attn_end(int qo, int qlen, int ctx, int qt, int t
   return min(qo + min(qlen, (qt + 1) * tq), ctx);
 }
 
-template <int D>
+// NT: K and V stream with the nt cache policy; used when each K/V row is read by one workgroup
+// only (one query tile: decode).
+template <int D, bool NT>
 __global__ void __launch_bounds__(64 * kAttnWaves)
 paged_attn_kernel(PagedAttnArgs a) {
   static_assert(D == 128, "head_dim 128: 16 chunks of 16 bytes per K/V row");
@@ -153,11 +155,14 @@ paged_attn_kernel(PagedAttnArgs a) {
     for (int bk = 0; bk < 2; ++bk) {
       const uint16_t* kp = a.k_pool + row_off(n0 + 16 * bk + n16) + 8 * grp;
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) kf[bk][kk] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
+      for (int kk = 0; kk < KK; ++kk)
+        kf[bk][kk] = NT ? load16_stream(kp + 32 * kk) : *reinterpret_cast<const uint4*>(kp + 32 * kk);
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      vr[i] = *reinterpret_cast<const uint4*>(a.v_pool + row_off(n0 + grp + 4 * i) + 8 * n16);
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t* vp = a.v_pool + row_off(n0 + grp + 4 * i) + 8 * n16;
+      vr[i] = NT ? load16_stream(vp) : *reinterpret_cast<const uint4*>(vp);
+    }
 
     // Scores: lane holds keys n0 + 16 bk + 4 grp + r of row n16.
     f32x4 st[2];
@@ -416,7 +421,9 @@ int launch_paged_attention(const uint16_t* q, int64_t sq_h, int64_t sq_t, const 
   const int64_t blocks = (int64_t)a.entries * a.HKV * pl.qtiles * pl.parts;
   if (blocks > 0x7fffffff) return LSE_E_RANGE;
   void* args[] = {&a};
-  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(&paged_attn_kernel<128>),
+  const void* fn = pl.qtiles == 1 ? reinterpret_cast<const void*>(&paged_attn_kernel<128, true>)
+                                  : reinterpret_cast<const void*>(&paged_attn_kernel<128, false>);
+  hipError_t err = hipLaunchKernel(fn,
                                    dim3((unsigned)blocks), dim3(64 * kAttnWaves), args, 0, stream);
   if (err == hipSuccess && pl.parts > 1) {
     const int64_t threads = (int64_t)a.entries * a.H * a.max_q_len * (128 / 8);

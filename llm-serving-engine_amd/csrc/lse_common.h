@@ -73,6 +73,13 @@ __device__ __forceinline__ BufferRsrc make_rsrc(const void* base, uint32_t bytes
 constexpr int kLoadDefault = 0;
 constexpr int kLoadStream = 2;
 
+// A 16-byte global load with the streaming (nt) cache policy.
+__device__ __forceinline__ uint4 load16_stream(const void* p) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 template <int POLICY = kLoadDefault>
 __device__ __forceinline__ uint4 buffer_load16(BufferRsrc r, uint32_t byte_offset) {
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
