@@ -322,7 +322,8 @@ static const void* tiled_fn() {
 
 // `decode`: a decode route's tile (one block row, M <= 64), whose weights stream with the nt
 // cache policy: on MI355X 7-12 % faster for the decode kernel's large weights, which share
-// that policy.
+// that policy, and 5-8 % for the 32 x 128 tile over gate_up. The split-K route keeps the default
+// policy for its W8A16 64 x 128 tile (down_proj at 64 tokens: 7 % slower with nt).
 template <bool I8, bool GLU>
 static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false) {
   if (decode) {
@@ -499,7 +500,7 @@ static int launch_deep_decode(const void* x, int64_t ldx, const int8_t* qp, cons
   a.part = ws;
   void* args[] = {&a};
   const hipError_t e =
-      hipLaunchKernel(tiled_kernel_for<I8, false>(sh, true),
+      hipLaunchKernel(tiled_kernel_for<I8, false>(sh, I8 || sh.bm == 32),
                       dim3((unsigned)(a.mblocks * a.nblocks * kDeepSplits)), dim3(256), args, 0,
                       stream);
   if (e != hipSuccess) return (int)e;
