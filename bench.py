@@ -906,9 +906,9 @@ def main() -> None:
         secondary["fused_gate_up"] = bench_glu(pkg, dev, args.steps, gen)
         secondary["paged_attention"] = bench_attention(pkg, dev, args.steps, gen)
 
-    cpu = None
+    cpu = cpu_int8 = None
     if not args.no_cpu and args.only is None:
-        from oracle.cpu_baseline import time_bf16_linear_sweep
+        from oracle.cpu_baseline import time_bf16_linear_sweep, time_int8_restatements
 
         c = time_bf16_linear_sweep(SHAPES, DECODE_MS, budget_s=20.0)
         cpu = {
@@ -918,6 +918,15 @@ def main() -> None:
             "kind": "port",
             "sample": ("reference path bf16 F.linear on the host CPU "
                        f"({c['cpu']}), one layer of each config-1 shape at M in {DECODE_MS}, "
+                       "median of 5"),
+        }
+        r = time_int8_restatements(SHAPES, DECODE_MS, budget_s=10.0)
+        cpu_int8 = {
+            "unit": "GB/s",
+            "cores": r["threads"],
+            "w8a16_weight_int8pack_mm": round(r["w8a16_weight_int8pack_mm"]["gbps"], 2),
+            "w8a8_quantize_int_mm": round(r["w8a8_int_mm"]["gbps"], 2),
+            "sample": ("torch's int8 CPU kernels for the same layers and M, same bytes unit, "
                        "median of 5"),
         }
 
@@ -951,6 +960,7 @@ def main() -> None:
             "traffic": measured_traffic(dec),
         },
         "cpu_baseline": cpu,
+        "cpu_int8_restatements": cpu_int8,
         "decode_by_m_gbps": dec["by_m_gbps"],
         "decode_by_shape": dec["by_shape"],
         **secondary,

@@ -560,3 +560,18 @@ def test_pack_bf16_weight_matches_the_layout_definition():
                     cols = 64 * j + 16 * g + 8 * h + np.arange(8)
                     y[:, 16 * rb + r] += xf[:, cols] @ pf[rb, j, h, lane].astype(np.float64)
     np.testing.assert_allclose(y[:, :n], ora.bf16_linear_golden(x, w), rtol=1e-12, atol=1e-12)
+
+
+def test_cpu_baselines_run_on_tiny_layers():
+    """bench.py's CPU legs (bf16 F.linear, and torch's int8 kernels beside it) time every case
+    and report bytes per second in the int8 layer's algorithmic bytes."""
+    from oracle.cpu_baseline import time_bf16_linear_sweep, time_int8_restatements
+
+    shapes, ms = [(64, 32), (128, 48)], [1, 3]
+    bf16 = time_bf16_linear_sweep(shapes, ms, budget_s=2.0)
+    assert len(bf16["cases"]) == 4 and bf16["gbps"] > 0
+    assert bf16["bytes"] == sum(k * n + 4 * n + 2 * m * k + 2 * m * n for k, n in shapes for m in ms)
+    r = time_int8_restatements(shapes, ms, budget_s=2.0)
+    assert r["threads"] >= 1
+    for name in ("w8a16_weight_int8pack_mm", "w8a8_int_mm"):
+        assert r[name]["gbps"] > 0 and r[name]["seconds"] > 0
