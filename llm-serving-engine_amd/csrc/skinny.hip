@@ -3,7 +3,8 @@
 //   W8A8:  acc[m,n] = sum_k xq[m,k] q[n,k] exactly in int32;  y = bf16((acc * sx[m]) * s[n])
 //
 // The kernel is a weight stream: every weight byte is read once from HBM, in packed tiles
-// (lse_common.h) so that each 128-bit load of a wave is one contiguous 1 KB tile.
+// (lse_common.h) so that each 128-bit load of a wave is one contiguous 1 KB tile, with the
+// streaming (nt) cache policy so the stream does not evict the activations and scales.
 //
 // Work decomposition.
 //  * A panel is RT row tiles (16 * RT weight rows). The K steps split into S ranges of `ssteps`

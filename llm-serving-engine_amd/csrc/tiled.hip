@@ -17,7 +17,10 @@
 //    the compiler does not track, so the only waits on them are the ones written here.
 //  * Weights stay int8 in LDS (half the footprint and fill traffic of bf16); in W8A16 each wave
 //    dequantizes its WN/16 tiles after the LDS read (exact: |q| <= 127), 1.5 VALU ops per
-//    weight, shared by the WM/16 token tiles it multiplies.
+//    weight, shared by the WM/16 token tiles it multiplies. With one wave row (WGM = 1) the
+//    weights travel one stage ahead of x and each stage's dequantization runs under the
+//    previous stage's MFMAs (WAHEAD).
+//  * Decode tiles (one block row, M <= 64) load weights with the streaming (nt) cache policy.
 //  * x rows are stored 16-byte-chunk swizzled (chunk c of row r at c ^ swz(r)) so the fragment
 //    reads of 16 rows at one K offset have no LDS bank conflicts (tiled_swz).
 //  * One barrier per stage: after it, the stage's loads from every wave have landed and every
