@@ -219,6 +219,23 @@ def bench_prefill(pkg, dev, steps: int, gen) -> dict:
         t = time_graph(step, 2) / LAYERS
         res[str(m)] = {"tflops": round(flops / t / 1e12, 1), "ms": round(t * 1e3, 3)}
     res["mfma_frac_M2048"] = round(res["2048"]["tflops"] / BF16_PEAK_TFLOPS, 4)
+    del weights
+    # Context, not the product: the vendor BLAS's bf16 GEMM (F.linear on bf16 weights, no
+    # dequantization) on the same shapes, rotated copies and graph replay.
+    w16 = [[(torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+            for _ in range(LAYERS)] for k, n in SHAPES]
+    for m in PREFILL_MS:
+        xs = [torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev) for k, _ in SHAPES]
+        flops = sum(2 * m * n * k for k, n in SHAPES)
+
+        def vstep(xs=xs):
+            for layer in range(LAYERS):
+                for x, copies in zip(xs, w16):
+                    torch.nn.functional.linear(x, copies[layer])
+
+        t = time_graph(vstep, 2) / LAYERS
+        res[str(m)]["vendor_bf16_tflops"] = round(flops / t / 1e12, 1)
+    del w16
     return res
 
 
