@@ -268,6 +268,28 @@ def bench_w8a8(pkg, dev, steps: int, gen) -> dict:
         t = time_graph(step, max(2, steps // 4)) / LAYERS
         res[str(m)] = {"tops": round(ops / t / 1e12, 2), "ms": round(t * 1e3, 4),
                        "gbps": round(nbytes / t / 1e9, 1)}
+    del weights
+    # Context, not the product: the vendor BLAS's int8 GEMM (torch._int_mm, int32 out, no
+    # quantizer or epilogue) on the same shapes at the prefill-sized M, rotated copies.
+    qv = [[torch.randint(-127, 128, (n, k), generator=gen, dtype=torch.int8).to(dev)
+           for _ in range(LAYERS)] for k, n in SHAPES]
+    for m in (mm for mm in W8A8_MS if mm >= 512):
+        xs = [torch.randint(-127, 128, (m, k), generator=gen, dtype=torch.int8).to(dev)
+              for k, _ in SHAPES]
+        ops = sum(2 * m * n * k for k, n in SHAPES)
+
+        def vstep(xs=xs):
+            for layer in range(LAYERS):
+                for x, copies in zip(xs, qv):
+                    torch._int_mm(x, copies[layer].t())
+
+        try:
+            t = time_graph(vstep, 2) / LAYERS
+            res[str(m)]["vendor_int_mm_tops"] = round(ops / t / 1e12, 1)
+        except RuntimeError as e:  # not every build routes _int_mm to a GPU kernel
+            res[str(m)]["vendor_int_mm_tops"] = None
+            print(f"[w8a8] vendor int8 GEMM unavailable: {e}", file=sys.stderr, flush=True)
+    del qv
     res["rmsnorm_quantize"] = bench_rmsnorm_quantize(pkg, dev, steps, gen)
     return res
 
