@@ -171,7 +171,8 @@ def test_output_stride_guard_band(pkg, dev, algo):
     assert ora.within_tolerance(y, ora.w8a16_golden(x_bits, q, s))[0]
 
 
-@pytest.mark.parametrize("k,n", [(4096, 512), (14336, 4096), (1024, 6144), (256, 16400)])
+@pytest.mark.parametrize(
+    "k,n", [(4096, 512), (14336, 4096), (1024, 6144), (8192, 6400), (256, 16400)])
 def test_decode_rows_are_batch_invariant(pkg, dev, k, n):
     """A row's result does not depend on M or on the other rows within a token class (M <= 16,
     17..32, 33..64): the graphed decode runs a padded power-of-two bucket while eager decode runs
