@@ -195,6 +195,30 @@ def bench_decode(pkg, dev, steps: int, warmup: int, gen) -> dict:
     }
 
 
+def bench_decode_reference(dev, steps: int, gen, int8_seconds: float) -> dict:
+    """The reference engine's own GPU path for the same sweep, as context: every projection a
+    bf16 `F.linear` on bf16 weights (model_runner.py:49, 184-200), same shapes, M, rotated
+    copies and graph replay. Returns its us per step and the int8 path's speedup over it."""
+    import torch
+
+    w16 = [[(torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+            for _ in range(LAYERS)] for k, n in SHAPES]
+    xs = {(m, k): torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+          for m in DECODE_MS for k in {k for k, _ in SHAPES}}
+
+    def step():
+        for m in DECODE_MS:
+            for layer in range(LAYERS):
+                for si, (k, _) in enumerate(SHAPES):
+                    torch.nn.functional.linear(xs[(m, k)], w16[si][layer])
+
+    t = time_graph(step, steps)
+    del w16
+    return {"bf16_us_per_step": round(t * 1e6, 1),
+            "int8_us_per_step": round(int8_seconds * 1e6, 1),
+            "speedup": round(t / int8_seconds, 3)}
+
+
 def bench_prefill(pkg, dev, steps: int, gen) -> dict:
     """Config 2: the four Llama-3-8B projections (one "layer") at M in PREFILL_MS through the
     tiled kernel, over LAYERS rotated weight copies, replayed from one captured graph as the
@@ -944,6 +968,8 @@ def main() -> None:
         secondary["w8a8"] = bench_w8a8(pkg, dev, args.steps, gen)
         secondary["fused_gate_up"] = bench_glu(pkg, dev, args.steps, gen)
         secondary["paged_attention"] = bench_attention(pkg, dev, args.steps, gen)
+        secondary["decode_vs_reference_bf16"] = bench_decode_reference(
+            dev, args.steps, gen, dec["seconds_per_step"])
 
     cpu = cpu_int8 = None
     if not args.no_cpu and args.only is None:
