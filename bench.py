@@ -45,6 +45,7 @@ BF16_PEAK_TFLOPS = 2500.0
 INT8_PEAK_TOPS = 5000.0
 SHAPES = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]  # (K, N)
 SHAPE_NAMES = ["qkv", "o_proj", "gate_up", "down"]
+KV_SHAPE = (4096, 1024)  # (K, N) of the separate k_proj and v_proj the drop-in runs
 DECODE_MS = [1, 8, 32, 64]
 PREFILL_MS = [512, 2048, 8192]
 W8A8_MS = [1, 32, 512, 4096]
@@ -140,7 +141,8 @@ def bench_decode(pkg, dev, steps: int, warmup: int, gen) -> dict:
     # the timed region measures the kernels, not host-side launch cost.
     # The launches run in order on one stream, so they share one workspace of the largest size.
     lib = pkg.library()
-    ws_bytes = max(lib.lse_workspace_bytes(0, m, n, k) for m in DECODE_MS for k, n in SHAPES)
+    ws_bytes = max(lib.lse_workspace_bytes(0, m, n, k) for m in DECODE_MS
+                   for k, n in SHAPES + [KV_SHAPE])
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     calls = []
     for m in DECODE_MS:
@@ -180,11 +182,22 @@ def bench_decode(pkg, dev, steps: int, warmup: int, gen) -> dict:
         by_m[str(m)] = round(b / t / 1e9, 1)
     by_shape = {}
     for si, (k, n) in enumerate(SHAPES):
-        for m in (1, 64):
+        for m in DECODE_MS:
             sub = [c for c in calls if c[:3] == (m, k, n)]
             t = time_region(graph_of(sub).replay, steps, 1) / (steps * len(sub))
             by_shape[f"{SHAPE_NAMES[si]}_M{m}"] = {
                 "us": round(t * 1e6, 2), "gbps": round(decode_bytes(m, k, n) / t / 1e9, 1)}
+    # The drop-in's own k_proj / v_proj (model_runner.py:322-324 calls q, k and v separately):
+    # (K, N) = (4096, 1024), over as many rotated copies as keep the same bytes beyond the cache.
+    k, n = KV_SHAPE
+    kv_weights = make_weights(pkg, dev, k, n, 4 * LAYERS, gen)
+    for m in DECODE_MS:
+        y_kv = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        sub = [(m, k, n, (xs[(m, k)].data_ptr(), k, q.data_ptr(), s.data_ptr(), y_kv.data_ptr(),
+                          n, m, n, k, 1, ws.data_ptr(), ws_bytes)) for q, s in kv_weights]
+        t = time_region(graph_of(sub).replay, steps, 1) / (steps * len(sub))
+        by_shape[f"kv_proj_M{m}"] = {
+            "us": round(t * 1e6, 2), "gbps": round(decode_bytes(m, k, n) / t / 1e9, 1)}
     return {
         "seconds_per_step": per_step,
         "bytes_per_step": total_bytes,
@@ -424,10 +437,13 @@ def bench_lm_head(pkg, dev, steps: int, gen) -> dict:
     return res
 
 
-ATTN_CASES = [  # (name, entries, context, pools rotated)
-    ("decode_b64_ctx1025", 64, 1025, 4),    # config 4's decode step, one layer
-    ("decode_b8_ctx8192", 8, 8192, 4),      # few sequences, long context: the split path
-    ("decode_b256_ctx512", 256, 512, 4),
+ATTN_CASES = [  # (name, entries, context, pools rotated, table as wide as the pool)
+    ("decode_b64_ctx1025", 64, 1025, 4, False),  # config 4's decode step, one layer
+    # the same call in the reference's graphed-decode shape (decode_graph.py:97,149): a block
+    # table as wide as the whole pool
+    ("decode_b64_ctx1025_pool_wide_table", 64, 1025, 4, True),
+    ("decode_b8_ctx8192", 8, 8192, 4, False),    # few sequences, long context: the split path
+    ("decode_b256_ctx512", 256, 512, 4, False),
 ]
 ATTN_H, ATTN_HKV, ATTN_D, ATTN_BS = 32, 8, 128, 16
 
@@ -442,11 +458,16 @@ def bench_attention(pkg, dev, steps: int, gen) -> dict:
 
     res = {}
     h, h_kv, d, bs = ATTN_H, ATTN_HKV, ATTN_D, ATTN_BS
-    for name, e, ctx, pools in ATTN_CASES:
+    for name, e, ctx, pools, pool_wide in ATTN_CASES:
         nblk = -(-ctx // bs)
         blocks = e * nblk + 1
         perm = torch.randperm(blocks - 1, generator=gen)
-        table = perm[: e * nblk].reshape(e, nblk).to(torch.int32).to(dev)
+        table = perm[: e * nblk].reshape(e, nblk).to(torch.int32)
+        if pool_wide:  # columns past each sequence's blocks name the scratch block
+            wide = torch.full((e, blocks), blocks - 1, dtype=torch.int32)
+            wide[:, :nblk] = table
+            table = wide
+        table = table.to(dev)
         kv = [(torch.randn(blocks, bs, h_kv, d, generator=gen).to(torch.bfloat16).to(dev),
                torch.randn(blocks, bs, h_kv, d, generator=gen).to(torch.bfloat16).to(dev))
               for _ in range(pools)]
@@ -759,7 +780,7 @@ def summarize_attention(trace_dir: str) -> None:
            "adds its paged_attn_merge pass.", "",
            "| case | sequences | context | grid | kernel us | merge us | algorithmic MB | GB/s | "
            "frac of 8 TB/s |", "|---|---|---|---|---|---|---|---|---|"]
-    for ci, (name, e, ctx, _pools) in enumerate(ATTN_CASES):
+    for ci, (name, e, ctx, _pools, _wide) in enumerate(ATTN_CASES):
         block = main[ci * per:(ci + 1) * per]
         t0, t1 = int(block[0]["Start_Timestamp"]), int(block[-1]["End_Timestamp"])
         ms = [dur(r) for r in merge if t0 <= int(r["Start_Timestamp"]) <= t1 + 1_000_000]
@@ -793,6 +814,45 @@ def measured_traffic(dec: dict) -> float | None:
     if t.get("calls") != dec["launches_per_step"]:
         return None
     return t["hbm_bytes_per_call"]
+
+
+def bench_eager_overhead(pkg, dev, steps: int, gen, calls: int = 500) -> dict:
+    """Host cost of eager `Int8Linear` calls (Python validation, the workspace query and
+    torch.empty, the ctypes launch), which an eager caller pays per projection (the reference's
+    forward_fused, model_runner.py:202-211, and the attention between piecewise segments): the
+    o_proj shape at M = 1, `calls` calls back to back. host_submit_us = host time per call
+    before the final synchronisation; eager_us = wall time per call including it; beside them
+    the same call replayed from a graph, and torch's eager bf16 F.linear on the same shape."""
+    import time
+
+    import torch
+
+    from llm_serving_engine_amd.int8_linear import Int8Linear
+
+    k, n = 4096, 4096
+    lin = torch.nn.Linear(k, n, bias=False, device=dev, dtype=torch.bfloat16)
+    mod = Int8Linear.from_linear(lin)
+    x = torch.randn(1, k, generator=gen).to(torch.bfloat16).to(dev)
+
+    def loop(fn):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        return (t1 - t0) / calls, (time.perf_counter() - t0) / calls
+
+    submit, eager = loop(lambda: mod(x))
+    f_submit, f_eager = loop(lambda: torch.nn.functional.linear(x, lin.weight))
+    graph = time_graph(lambda: mod(x), steps)
+    return {"shape": "o_proj (4096, 4096), M = 1", "calls": calls,
+            "host_submit_us": round(submit * 1e6, 2), "eager_us": round(eager * 1e6, 2),
+            "graph_replay_us": round(graph * 1e6, 2),
+            "bf16_F_linear_host_submit_us": round(f_submit * 1e6, 2),
+            "bf16_F_linear_eager_us": round(f_eager * 1e6, 2)}
 
 
 def time_graph(fn, steps: int) -> float:
@@ -861,6 +921,25 @@ def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
         top = logits.argmax(-1)
         match += int((top == ref_top[t]).sum())
         match_torch += int((top == restated.argmax(-1)).sum())
+    # Layer-wise error: each projection of one step against the fp64 product of the input the
+    # kernel saw (gate_up: fp64 silu(g) * u), as max|y - golden| / max|golden|.
+    runner.trace = []
+    runner.step(inputs[-1], context + decode_steps - 1)
+    worst = 0.0
+    for i, name, x, y in runner.trace:
+        mod = runner.int8[i][name]
+        q, s = mod.unpacked_qweight().double(), mod.scales.double()
+        xd = x.reshape(-1, x.shape[-1]).double()
+        if name == "gate_up":
+            inter = mod.intermediate_size
+            g = (xd @ q[:inter].t()) * s[:inter]
+            golden = torch.nn.functional.silu(g) * ((xd @ q[inter:].t()) * s[inter:])
+        else:
+            golden = (xd @ q.t()) * s
+        err = (y.reshape(golden.shape).double() - golden).abs().max() / golden.abs().max()
+        worst = max(worst, float(err))
+    traced = len(runner.trace)
+    runner.trace = None
     int8_calls = runner.linear_calls(batch)
     int8_bytes = runner.linear_bytes(batch)
     t_int8 = time_graph(lambda: [mod(x) for mod, x in int8_calls], steps)
@@ -905,6 +984,8 @@ def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
         "greedy_match_rate_vs_int8_torch_restatement": round(
             match_torch / (batch * decode_steps), 4),
         "logit_rel_diff_vs_int8_torch_restatement": round(max(rel), 5),
+        "layerwise_projections_checked": traced,
+        "layerwise_worst_max_abs_over_max_golden": round(worst, 6),
         "tokens_compared": batch * decode_steps,
         "top2_margin_over_logit_std": {"median": round(float(margin.median()), 4),
                                        "min": round(float(margin.min()), 5)},
@@ -970,6 +1051,9 @@ def main() -> None:
         secondary["paged_attention"] = bench_attention(pkg, dev, args.steps, gen)
         secondary["decode_vs_reference_bf16"] = bench_decode_reference(
             dev, args.steps, gen, dec["seconds_per_step"])
+        secondary["eager_int8_linear"] = bench_eager_overhead(pkg, dev, args.steps, gen)
+        torch.cuda.empty_cache()
+        secondary["decode_step"] = bench_decode_step(pkg, dev, args.steps)
 
     cpu = cpu_int8 = None
     if not args.no_cpu and args.only is None:

@@ -255,9 +255,13 @@ int64_t lse_paged_attention_workspace_bytes(int64_t entries, int64_t H, int64_t 
  *   query_offset, q_start, q_len: (entries) int32. Their values must describe positions inside
  *   the pool and rows inside q/o (the kernel reads only blocks the table names for positions
  *   below context_len), as for the reference kernel.
- * Shapes: D = 128; H a multiple of H_KV with H / H_KV in {1, 2, 4, 8, 16}; strides multiples of 8
+ * Shapes: D = 128; H a multiple of H_KV with 1 <= H / H_KV <= 16; strides multiples of 8
  *   elements and base pointers 16-byte aligned. max_q_len >= every q_len (a graphed decode may
  *   pass its bucket size). workspace as sized by lse_paged_attention_workspace_bytes.
+ * Determinism: each row's keys are summed in fixed 512-position chunks, merged in a fixed order,
+ *   so a row's output does not depend on the other entries, the entry count, max_q_len or the
+ *   table width (a graph bucket with q_len = 0 padding rows and a pool-wide table gives the bits
+ *   an exact-width eager call gives).
  * Replaces: `paged_attention_forward` (src/llm_serving_engine/kernels/flash_attention.py:
  *   287-332, the Triton kernel `paged_attention_2` at :201-284), called from
  *   `ModelRunner.attend_paged` (model_runner.py:357-363).

@@ -11,7 +11,8 @@ weights on the GPU as they arrive.
 
 Format (one safetensors file, little-endian, no pickled objects):
   * `<module>.qweight`: int8 (N, K) row-major per-output-channel weight of each quantized
-    projection, `<module>.scales`: fp32 (N,), under the HF module names
+    projection, `<module>.scales`: fp32 (N,), and `<module>.bias` (bf16, when the projection has
+    one: `attention_bias` / `mlp_bias` configs), under the HF module names
     (`model.layers.{i}.self_attn.q_proj`, ..., `model.layers.{i}.mlp.down_proj`); a fused
     gate/up is stored as its two projections;
   * every other parameter under its HF name, bf16;
@@ -31,43 +32,59 @@ from . import ops
 from .int8_linear import Int8GateUp, Int8GluMLP, Int8Linear, Int8RMSNormQuant
 
 FORMAT = "lse-int8"
+MODEL_TYPES = ("llama",)  # architectures the loader rebuilds (LlamaForCausalLM)
 FORMAT_VERSION = "1"
 ATTENTION = ("q_proj", "k_proj", "v_proj", "o_proj")
 MLP = ("gate_proj", "up_proj", "down_proj")
 
 
+def _check_model_type(model_type: str | None) -> None:
+    if model_type not in MODEL_TYPES:
+        raise RuntimeError(f"int8 checkpoints rebuild {MODEL_TYPES} models, not {model_type!r}")
+
+
+def _fused_mlp(config) -> bool:
+    """Whether the loader rebuilds a layer's MLP as the fused `Int8GluMLP` (what
+    `quantize_model_` builds for a bias-free SiLU MLP) or as three `Int8Linear` projections."""
+    return not getattr(config, "mlp_bias", False) and getattr(config, "hidden_act", "silu") == "silu"
+
+
 def _quantized_tensors(model: nn.Module) -> tuple[dict[str, torch.Tensor], str]:
-    """name -> CPU tensor for every quantized projection, and the model's mode."""
+    """name -> CPU tensor for every quantized projection (weight, scales and bias when present),
+    and the model's mode."""
     out: dict[str, torch.Tensor] = {}
     modes = set()
+
+    def put(prefix: str, mod: Int8Linear) -> None:
+        out[f"{prefix}.qweight"] = mod.unpacked_qweight().cpu()
+        out[f"{prefix}.scales"] = mod.scales.cpu()
+        if mod.bias is not None:
+            out[f"{prefix}.bias"] = mod.bias.detach().to(torch.bfloat16).cpu().contiguous()
+        modes.add(mod.mode)
+
     for i, layer in enumerate(model.model.layers):
         prefix = f"model.layers.{i}"
         for name in ATTENTION:
             mod = getattr(layer.self_attn, name)
             if not isinstance(mod, Int8Linear):
                 raise RuntimeError(f"{prefix}.self_attn.{name} is not quantized")
-            out[f"{prefix}.self_attn.{name}.qweight"] = mod.unpacked_qweight().cpu()
-            out[f"{prefix}.self_attn.{name}.scales"] = mod.scales.cpu()
-            modes.add(mod.mode)
+            put(f"{prefix}.self_attn.{name}", mod)
         mlp = layer.mlp
         if isinstance(mlp, Int8GluMLP):
             gu = mlp.gate_up
             q, s, inter = gu.unpacked_qweight().cpu(), gu.scales.cpu(), gu.intermediate_size
-            parts = {"gate_proj": (q[:inter], s[:inter]), "up_proj": (q[inter:], s[inter:]),
-                     "down_proj": (mlp.down_proj.unpacked_qweight().cpu(),
-                                   mlp.down_proj.scales.cpu())}
-            modes.update((gu.mode, mlp.down_proj.mode))
+            for name, (q_part, s_part) in (("gate_proj", (q[:inter], s[:inter])),
+                                           ("up_proj", (q[inter:], s[inter:]))):
+                out[f"{prefix}.mlp.{name}.qweight"] = q_part.contiguous()
+                out[f"{prefix}.mlp.{name}.scales"] = s_part.contiguous()
+            modes.add(gu.mode)
+            put(f"{prefix}.mlp.down_proj", mlp.down_proj)
         else:
-            parts = {}
             for name in MLP:
                 mod = getattr(mlp, name)
                 if not isinstance(mod, Int8Linear):
                     raise RuntimeError(f"{prefix}.mlp.{name} is not quantized")
-                parts[name] = (mod.unpacked_qweight().cpu(), mod.scales.cpu())
-                modes.add(mod.mode)
-        for name, (q, s) in parts.items():
-            out[f"{prefix}.mlp.{name}.qweight"] = q.contiguous()
-            out[f"{prefix}.mlp.{name}.scales"] = s.contiguous()
+                put(f"{prefix}.mlp.{name}", mod)
     if len(modes) != 1:
         raise RuntimeError(f"mixed quantization modes {sorted(modes)}")
     return out, modes.pop()
@@ -77,6 +94,7 @@ def save_int8_checkpoint(model: nn.Module, path: str | Path) -> Path:
     """Writes a model quantized by `quantize_model_` to `path` (a .safetensors file)."""
     from safetensors.torch import save_file
 
+    _check_model_type(getattr(model.config, "model_type", None))
     tensors, mode = _quantized_tensors(model)
     for name, t in model.state_dict().items():
         if t.is_floating_point() and not name.endswith((".qweight", ".scales")):
@@ -129,36 +147,46 @@ def load_int8_checkpoint(path: str | Path, device: torch.device | str = "cuda") 
     meta = read_metadata(path)
     mode = meta["mode"]
     cfg_dict = json.loads(meta["config"])
+    _check_model_type(cfg_dict.get("model_type"))
     config = AutoConfig.for_model(**cfg_dict)
     device = torch.device(device)
     with torch.device("meta"):
         model = LlamaForCausalLM._from_config(config, dtype=torch.bfloat16)
     model.eval()
     hidden, inter = config.hidden_size, config.intermediate_size
+    fused = _fused_mlp(config)
     with safe_open(str(path), framework="pt", device="cpu") as f:
+        keys = set(f.keys())
+
         def load_q(name: str) -> tuple[torch.Tensor, torch.Tensor]:
             return (f.get_tensor(f"{name}.qweight").to(device),
                     f.get_tensor(f"{name}.scales").to(device))
 
+        def linear(name: str) -> Int8Linear:
+            q, s = load_q(name)
+            bias = f.get_tensor(f"{name}.bias").to(device) if f"{name}.bias" in keys else None
+            return Int8Linear.from_quantized(q, s, mode, bias)
+
         for i, layer in enumerate(model.model.layers):
             prefix = f"model.layers.{i}"
             for name in ATTENTION:
-                q, s = load_q(f"{prefix}.self_attn.{name}")
-                setattr(layer.self_attn, name, Int8Linear.from_quantized(q, s, mode))
-                del q
-            qg, sg = load_q(f"{prefix}.mlp.gate_proj")
-            qu, su = load_q(f"{prefix}.mlp.up_proj")
-            gate_up = Int8GateUp.from_quantized(torch.cat([qg, qu]), torch.cat([sg, su]), mode)
-            del qg, qu
-            qd, sd = load_q(f"{prefix}.mlp.down_proj")
-            layer.mlp = Int8GluMLP(gate_up, Int8Linear.from_quantized(qd, sd, mode))
-            del qd
-            assert gate_up.in_features == hidden and gate_up.intermediate_size == inter
+                setattr(layer.self_attn, name, linear(f"{prefix}.self_attn.{name}"))
+            if fused:
+                qg, sg = load_q(f"{prefix}.mlp.gate_proj")
+                qu, su = load_q(f"{prefix}.mlp.up_proj")
+                gate_up = Int8GateUp.from_quantized(torch.cat([qg, qu]), torch.cat([sg, su]),
+                                                    mode)
+                del qg, qu
+                layer.mlp = Int8GluMLP(gate_up, linear(f"{prefix}.mlp.down_proj"))
+                assert gate_up.in_features == hidden and gate_up.intermediate_size == inter
+            else:  # the config's own MLP (act_fn, biases) around three int8 projections
+                for name in MLP:
+                    setattr(layer.mlp, name, linear(f"{prefix}.mlp.{name}"))
         # Everything still on the meta device is a bf16 parameter or buffer of the checkpoint,
         # or a buffer computed at construction (the rotary frequencies), rebuilt below. Only
         # those are materialized: the int8 buffers above stay as loaded.
         _materialize_meta(model, device)
-        names = {n for n in f.keys() if not n.endswith((".qweight", ".scales"))}
+        names = {n for n in keys if not n.endswith((".qweight", ".scales"))}
         for name, p in list(model.named_parameters()) + list(model.named_buffers()):
             if name in names:
                 p.copy_(f.get_tensor(name).to(p.dtype))

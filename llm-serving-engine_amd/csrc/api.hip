@@ -365,8 +365,7 @@ int check_attention_sizes(int64_t entries, int64_t H, int64_t HKV, int64_t D, in
       entries > kMaxRows || H > 65536 || max_q_len > kMaxRows)
     return LSE_E_SHAPE;
   if (D != 128 || H % HKV) return LSE_E_SHAPE;
-  const int64_t g = H / HKV;
-  if (g != 1 && g != 2 && g != 4 && g != 8 && g != 16) return LSE_E_SHAPE;
+  if (H / HKV > 16) return LSE_E_SHAPE;  // a query tile holds at least one token's group
   if (max_blocks * block_size > kMaxRows) return LSE_E_RANGE;
   return LSE_OK;
 }

@@ -10,13 +10,20 @@
 // Like the reference, the softmax runs online in fp32 and the probabilities are rounded to bf16
 // before the product with V (fp32 accumulation); the output is rounded to bf16.
 //
-// Work decomposition. A workgroup of four waves takes one (entry, K/V head, query tile, key
-// partition). A query tile is 16 MFMA rows: 16 / G query tokens x the G query heads that share
-// the K/V head (GQA), so every K/V byte a workgroup reads serves all G heads. The partition's keys
-// go to the waves in tiles of 32, round-robin; each wave keeps its own online-softmax state and
-// the four are merged through LDS at the end. Long contexts with few (entry, head, tile) items are
-// split into key partitions whose partial results (unnormalized O, running max and sum) a second
-// kernel merges; the split depends only on the shapes, never on the data.
+// Work decomposition. A workgroup of four waves takes one (entry, K/V head, query tile) item, or
+// one key chunk of it. A query tile is 16 MFMA rows: TQ = floor(16 / G) query tokens x the G query
+// heads that share the K/V head (GQA), so every K/V byte a workgroup reads serves all G heads; with
+// G not dividing 16 (e.g. 24 query heads over 8 K/V heads) the last 16 - TQ G rows are idle.
+//
+// Canonical order of summation. A row's keys are cut into chunks of kAttnChunk positions
+// (0..511, 512..1023, ...), fixed lengths that depend on nothing but the position. Within a chunk
+// the four waves take 32-key tiles round-robin, each keeping its own online-softmax state, and the
+// four states are merged in wave order; the chunks' merged states are then folded in chunk order
+// (attn_fold). Whether the chunks of an item run one after another in one workgroup or as
+// separate workgroups whose states a second kernel folds (the split launch, chosen from the shapes
+// to fill the CUs) changes only where the arithmetic runs, never the arithmetic: a row's output is
+// bit-identical whatever the batch around it, the table width or the query bucket, as for the
+// reference's kernel, which never splits a row.
 //
 // Per 32-key tile and wave:
 //  * S^T = K Q^T on v_mfma_f32_16x16x32_bf16: K rows are the A operand (16 keys x 32 head dims:
@@ -37,8 +44,10 @@
 namespace lse {
 
 constexpr int kAttnWaves = 4;
-constexpr int kAttnKeys = 32;                          // keys per wave tile
-constexpr int kAttnPartKeys = kAttnWaves * kAttnKeys;  // partition lengths are multiples of this
+constexpr int kAttnKeys = 32;     // keys per wave tile
+constexpr int kAttnChunk = 512;   // keys per chunk of the canonical order
+constexpr int kAttnMaxSplit = 64;  // chunks per item the split launch takes at most
+static_assert(kAttnChunk % (kAttnWaves * kAttnKeys) == 0, "whole rounds of wave tiles per chunk");
 
 struct PagedAttnArgs {
   const uint16_t* q;  // bf16, element (h, t, d) at h * sq_h + t * sq_t + d
@@ -55,12 +64,12 @@ struct PagedAttnArgs {
   uint16_t* o;  // bf16, same indexing as q with strides so_h, so_t
   int64_t so_h, so_t;
   int entries, H, HKV, G, block_size, max_q_len;
-  int qtiles;        // ceil(max_q_len / (16 / G))
-  int parts;         // key partitions
-  int chunk;         // keys per partition (a multiple of kAttnPartKeys)
+  int tq;            // query tokens per tile: floor(16 / G)
+  int qtiles;        // ceil(max_q_len / tq)
+  int parts;         // 1: a workgroup folds every chunk of its item; > 1: one chunk per workgroup
   float scale_log2;  // softmax scale x log2(e): scores are kept in the base-2 domain
-  float* ws_o;       // parts > 1: partial O [parts][entries][H][max_q_len][D], fp32
-  float* ws_ml;      // parts > 1: running max and sum [parts][entries][H][max_q_len][2]
+  float* ws_o;       // parts > 1: chunk states' O [parts][entries][H][max_q_len][D], fp32
+  float* ws_ml;      // parts > 1: chunk states' max and sum [parts][entries][H][max_q_len][2]
 };
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -74,11 +83,40 @@ __device__ __forceinline__ bf16x4 lds_read_tr16(const unsigned char* p) {
 
 __device__ __forceinline__ float exp2_fast(float v) { return __builtin_amdgcn_exp2f(v); }
 
-// The keys [pstart, pend) a workgroup covers and the tile's causal bound: the furthest position any
-// of its rows attends to is query_offset + min(q_len, (qt + 1) * TQ) - 1, and never past
-// context_len.
+// The tile's causal bound: the furthest position any of its rows attends to is query_offset +
+// min(q_len, (qt + 1) * TQ) - 1, and never past context_len. Keys [0, attn_end) are its chunks'.
 __device__ __forceinline__ int attn_end(int qo, int qlen, int ctx, int qt, int tq) {
   return min(qo + min(qlen, (qt + 1) * tq), ctx);
+}
+
+__device__ __forceinline__ int attn_chunks(int end_n) {
+  return max(1, (end_n + kAttnChunk - 1) / kAttnChunk);
+}
+
+// Folds the next chunk's state (max mc in the base-2 domain, sum lc of exp2(s - mc), unnormalized
+// output oc) into the running state (M, L, O) of the chunks before it. From (-inf, 0, 0) the first
+// fold yields the chunk's state exactly. Explicit fused multiply-adds keep the arithmetic the same
+// in every kernel that folds.
+__device__ __forceinline__ void attn_fold(float& M, float& L, float (&O)[8], float mc, float lc,
+                                          const float* oc) {
+  const float mn = fmaxf(M, mc);
+  const float ref = mn == -__builtin_huge_valf() ? 0.0f : mn;  // no key yet: keep p = 0
+  const float fa = exp2_fast(M - ref), fb = exp2_fast(mc - ref);
+  L = __builtin_fmaf(lc, fb, L * fa);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) O[i] = __builtin_fmaf(oc[i], fb, O[i] * fa);
+  M = mn;
+}
+
+// Eight normalized outputs in bf16 (a row that saw no key gives zeros).
+__device__ __forceinline__ uint4 attn_out8(float L, const float (&O)[8]) {
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  uint4 out;
+  out.x = pack_bf16x2(O[0] * inv, O[1] * inv);
+  out.y = pack_bf16x2(O[2] * inv, O[3] * inv);
+  out.z = pack_bf16x2(O[4] * inv, O[5] * inv);
+  out.w = pack_bf16x2(O[6] * inv, O[7] * inv);
+  return out;
 }
 
 // NT: K and V stream with the nt cache policy; used when each K/V row is read by one workgroup
@@ -90,7 +128,8 @@ paged_attn_kernel(PagedAttnArgs a) {
   constexpr int W = kAttnWaves, KT = kAttnKeys, KK = D / 32, DT = D / 16;
   constexpr int VROWB = 2 * D;  // bytes of one V row in LDS
   constexpr float NEG_INF = -__builtin_huge_valf();
-  // Per wave: the V tile (32 rows), reused at the end for the wave's O (16 rows x D fp32).
+  // Per wave: the V tile (32 rows), reused at the end of a chunk for the wave's O (16 rows x D
+  // fp32).
   static_assert(KT * VROWB == 16 * D * 4, "the V tile and the O tile share one LDS region");
   __shared__ __attribute__((aligned(16))) unsigned char vbuf[W][KT * VROWB];
   __shared__ float mbuf[W][16], lbuf[W][16];
@@ -106,19 +145,23 @@ paged_attn_kernel(PagedAttnArgs a) {
   b /= a.qtiles;
   const int kvh = b % a.HKV;
   const int e = b / a.HKV;
-  const int G = a.G, TQ = 16 / G;
+  const int G = a.G, TQ = a.tq;
   const int qlen = a.q_len[e];
   if (qt * TQ >= qlen) return;
   const int ctx = a.context_len[e], qo = a.query_offset[e], qs = a.q_start[e];
   const int end_n = attn_end(qo, qlen, ctx, qt, TQ);
-  const int pstart = part * a.chunk;
-  const int pend = min(pstart + a.chunk, end_n);
-  if (part > 0 && pstart >= pend) return;  // beyond the tile's keys: the merge reads no result
+  const int nch = attn_chunks(end_n);
+  // Split launch: this workgroup's chunk only (none past the tile's keys: the fold reads no
+  // state there). Otherwise every chunk of the item, folded here.
+  const int c_first = a.parts > 1 ? part : 0;
+  const int c_end = a.parts > 1 ? part + 1 : nch;
+  if (c_first >= nch) return;
 
-  // This lane's MFMA row (for Q, the scores and the softmax state): token tq, head g of the group.
+  // This lane's MFMA row (for Q, the scores and the softmax state): token tq, head gq of the group.
+  // Rows from TQ G on are idle (G not dividing 16).
   const int tq = n16 / G, gq = n16 - tq * G;
   const int m_row = qt * TQ + tq;
-  const bool row_ok = m_row < qlen;
+  const bool row_ok = n16 < TQ * G && m_row < qlen;
   const int qpos = qo + m_row;  // the row's cache position: it sees keys n <= qpos
   const int head = kvh * G + gq;
 
@@ -133,163 +176,171 @@ paged_attn_kernel(PagedAttnArgs a) {
   }
   const int32_t* bt = a.block_table + (int64_t)e * a.sbt;
   const int bs = a.block_size;
-  // Element offset of key n's row (this K/V head) in the pool; keys past the partition are
-  // clamped to its last key, so every load stays inside the entry's own blocks.
-  auto row_off = [&](int n) -> int64_t {
-    n = min(n, pend - 1);
-    const int blk = bt[n / bs];
-    return (int64_t)blk * a.sb + (int64_t)(n - (n / bs) * bs) * a.sw + (int64_t)kvh * a.sh;
-  };
 
-  float m_run = NEG_INF, l_run = 0.0f;
-  f32x4 oacc[DT];
-#pragma unroll
-  for (int t = 0; t < DT; ++t) oacc[t] = f32x4{0, 0, 0, 0};
-  unsigned char* vb = vbuf[wave];
-
-  for (int n0 = pstart + KT * wave; n0 < pend; n0 += KT * W) {
-    // K rows of the tile's two 16-key blocks (A operand) and the V tile (16 bytes x 8 per lane:
-    // row (lane / 16) + 4 i, chunk lane % 16), all issued before any use.
-    uint4 kf[2][KK], vr[8];
-#pragma unroll
-    for (int bk = 0; bk < 2; ++bk) {
-      const uint16_t* kp = a.k_pool + row_off(n0 + 16 * bk + n16) + 8 * grp;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        kf[bk][kk] = NT ? load16_stream(kp + 32 * kk) : *reinterpret_cast<const uint4*>(kp + 32 * kk);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint16_t* vp = a.v_pool + row_off(n0 + grp + 4 * i) + 8 * n16;
-      vr[i] = NT ? load16_stream(vp) : *reinterpret_cast<const uint4*>(vp);
-    }
-
-    // Scores: lane holds keys n0 + 16 bk + 4 grp + r of row n16.
-    f32x4 st[2];
-#pragma unroll
-    for (int bk = 0; bk < 2; ++bk) {
-      st[bk] = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) st[bk] = mfma16x16x32(as_bf16x8(kf[bk][kk]), qf[kk], st[bk]);
-    }
-    float s[8];
-    float tmax = NEG_INF;
-#pragma unroll
-    for (int bk = 0; bk < 2; ++bk)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = n0 + 16 * bk + 4 * grp + r;
-        const bool ok = row_ok && n < pend && n <= qpos;
-        s[4 * bk + r] = ok ? st[bk][r] * a.scale_log2 : NEG_INF;
-        tmax = fmaxf(tmax, s[4 * bk + r]);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float mref = m_new == NEG_INF ? 0.0f : m_new;  // a row with no key yet keeps p = 0
-    const float alpha = exp2_fast(m_run - mref);
-    float p[8], psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      p[i] = exp2_fast(s[i] - mref);
-      psum += p[i];
-    }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    // O rows are 4 grp + r: their factors come from the lanes holding those rows.
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float ar = __shfl(alpha, 4 * grp + r);
-#pragma unroll
-      for (int t = 0; t < DT; ++t) oacc[t][r] *= ar;
-    }
-    bf16x8 pa;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) pa[i] = (__bf16)p[i];
-
-    // V tile to LDS: row rr = grp + 4 i, logical chunk n16 at physical chunk n16 ^ 2 (rr & 3).
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int rr = grp + 4 * i;
-      *reinterpret_cast<uint4*>(vb + rr * VROWB + 16 * (n16 ^ (2 * (rr & 3)))) = vr[i];
-    }
-    // O += P V. Group grp reads rows kb + (n16 >> 2), kb = 4 grp (keys 0..3 of its contraction
-    // slice) and 16 + 4 grp (keys 4..7), at logical columns 16 t + 4 (n16 & 3).
-    const int rlo = n16 >> 2;
-    const int swz = 2 * (rlo & 3);
-    const int cbyte = 8 * (n16 & 1);
-    const unsigned char* r0 = vb + (4 * grp + rlo) * VROWB + cbyte;
-    const unsigned char* r1 = vb + (16 + 4 * grp + rlo) * VROWB + cbyte;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      const int pc = (2 * t + ((n16 & 3) >> 1)) ^ swz;
-      const bf16x4 v0 = lds_read_tr16(r0 + 16 * pc);
-      const bf16x4 v1 = lds_read_tr16(r1 + 16 * pc);
-      const bf16x8 vv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-      oacc[t] = mfma16x16x32(pa, vv, oacc[t]);
-    }
-  }
-
-  // Merge the waves: each writes its state (O rows 4 grp + r, columns 16 t + n16) to its LDS region.
-  float* ob = reinterpret_cast<float*>(vb);
-  if (lane < 16) {
-    mbuf[wave][lane] = m_run;
-    lbuf[wave][lane] = l_run;
-  }
-#pragma unroll
-  for (int t = 0; t < DT; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) ob[(4 * grp + r) * D + 16 * t + n16] = oacc[t][r];
-  __syncthreads();
-
-  // 256 threads: row = tid / 16, columns 8 c .. 8 c + 7 with c = tid % 16.
+  // The thread's part of a chunk merge and of the output: row `row` of the tile (token row / G,
+  // head row % G), columns c8 .. c8 + 7.
   const int row = threadIdx.x >> 4, c8 = 8 * (threadIdx.x & 15);
   const int m_out = qt * TQ + row / G;
-  if (m_out >= qlen) return;
+  const bool out_ok = row < TQ * G && m_out < qlen;
   const int h_out = kvh * G + row % G;
-  float mw[W], M = NEG_INF;
+  float Mr = NEG_INF, Lr = 0.0f, Or[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  unsigned char* vb = vbuf[wave];
+
+  for (int c = c_first; c < c_end; ++c) {
+    const int pstart = c * kAttnChunk;
+    const int pend = min(pstart + kAttnChunk, end_n);
+    // Element offset of key n's row (this K/V head) in the pool; keys past the chunk are clamped
+    // to its last key, so every load stays inside the entry's own blocks.
+    auto row_off = [&](int n) -> int64_t {
+      n = min(n, pend - 1);
+      const int blk = bt[n / bs];
+      return (int64_t)blk * a.sb + (int64_t)(n - (n / bs) * bs) * a.sw + (int64_t)kvh * a.sh;
+    };
+
+    float m_run = NEG_INF, l_run = 0.0f;
+    f32x4 oacc[DT];
 #pragma unroll
-  for (int w = 0; w < W; ++w) {
-    mw[w] = mbuf[w][row];
-    M = fmaxf(M, mw[w]);
-  }
-  const float Mref = M == NEG_INF ? 0.0f : M;
-  float L = 0.0f, ov[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int t = 0; t < DT; ++t) oacc[t] = f32x4{0, 0, 0, 0};
+
+    for (int n0 = pstart + KT * wave; n0 < pend; n0 += KT * W) {
+      // K rows of the tile's two 16-key blocks (A operand) and the V tile (16 bytes x 8 per lane:
+      // row (lane / 16) + 4 i, chunk lane % 16), all issued before any use.
+      uint4 kf[2][KK], vr[8];
 #pragma unroll
-  for (int w = 0; w < W; ++w) {
-    const float f = exp2_fast(mw[w] - Mref);
-    L += f * lbuf[w][row];
-    const float* src = reinterpret_cast<const float*>(vbuf[w]) + row * D + c8;
+      for (int bk = 0; bk < 2; ++bk) {
+        const uint16_t* kp = a.k_pool + row_off(n0 + 16 * bk + n16) + 8 * grp;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ov[i] += f * src[i];
+        for (int kk = 0; kk < KK; ++kk)
+          kf[bk][kk] =
+              NT ? load16_stream(kp + 32 * kk) : *reinterpret_cast<const uint4*>(kp + 32 * kk);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint16_t* vp = a.v_pool + row_off(n0 + grp + 4 * i) + 8 * n16;
+        vr[i] = NT ? load16_stream(vp) : *reinterpret_cast<const uint4*>(vp);
+      }
+
+      // Scores: lane holds keys n0 + 16 bk + 4 grp + r of row n16.
+      f32x4 st[2];
+#pragma unroll
+      for (int bk = 0; bk < 2; ++bk) {
+        st[bk] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          st[bk] = mfma16x16x32(as_bf16x8(kf[bk][kk]), qf[kk], st[bk]);
+      }
+      float s[8];
+      float tmax = NEG_INF;
+#pragma unroll
+      for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = n0 + 16 * bk + 4 * grp + r;
+          const bool ok = row_ok && n < pend && n <= qpos;
+          s[4 * bk + r] = ok ? st[bk][r] * a.scale_log2 : NEG_INF;
+          tmax = fmaxf(tmax, s[4 * bk + r]);
+        }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float m_new = fmaxf(m_run, tmax);
+      const float mref = m_new == NEG_INF ? 0.0f : m_new;  // a row with no key yet keeps p = 0
+      const float alpha = exp2_fast(m_run - mref);
+      float p[8], psum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = exp2_fast(s[i] - mref);
+        psum += p[i];
+      }
+      psum += __shfl_xor(psum, 16);
+      psum += __shfl_xor(psum, 32);
+      l_run = __builtin_fmaf(l_run, alpha, psum);
+      m_run = m_new;
+      // O rows are 4 grp + r: their factors come from the lanes holding those rows.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * grp + r);
+#pragma unroll
+        for (int t = 0; t < DT; ++t) oacc[t][r] *= ar;
+      }
+      bf16x8 pa;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pa[i] = (__bf16)p[i];
+
+      // V tile to LDS: row rr = grp + 4 i, logical chunk n16 at physical chunk n16 ^ 2 (rr & 3).
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int rr = grp + 4 * i;
+        *reinterpret_cast<uint4*>(vb + rr * VROWB + 16 * (n16 ^ (2 * (rr & 3)))) = vr[i];
+      }
+      // O += P V. Group grp reads rows kb + (n16 >> 2), kb = 4 grp (keys 0..3 of its contraction
+      // slice) and 16 + 4 grp (keys 4..7), at logical columns 16 t + 4 (n16 & 3).
+      const int rlo = n16 >> 2;
+      const int swz = 2 * (rlo & 3);
+      const int cbyte = 8 * (n16 & 1);
+      const unsigned char* r0 = vb + (4 * grp + rlo) * VROWB + cbyte;
+      const unsigned char* r1 = vb + (16 + 4 * grp + rlo) * VROWB + cbyte;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const int pc = (2 * t + ((n16 & 3) >> 1)) ^ swz;
+        const bf16x4 v0 = lds_read_tr16(r0 + 16 * pc);
+        const bf16x4 v1 = lds_read_tr16(r1 + 16 * pc);
+        const bf16x8 vv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[t] = mfma16x16x32(pa, vv, oacc[t]);
+      }
+    }
+
+    // Merge the waves in wave order: each writes its state (O rows 4 grp + r, columns
+    // 16 t + n16) to its LDS region.
+    float* ob = reinterpret_cast<float*>(vb);
+    if (lane < 16) {
+      mbuf[wave][lane] = m_run;
+      lbuf[wave][lane] = l_run;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ob[(4 * grp + r) * D + 16 * t + n16] = oacc[t][r];
+    __syncthreads();
+
+    float mw[W], mc = NEG_INF;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      mw[w] = mbuf[w][row];
+      mc = fmaxf(mc, mw[w]);
+    }
+    const float mcref = mc == NEG_INF ? 0.0f : mc;
+    float lc = 0.0f, oc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = exp2_fast(mw[w] - mcref);
+      lc = __builtin_fmaf(f, lbuf[w][row], lc);
+      const float* src = reinterpret_cast<const float*>(vbuf[w]) + row * D + c8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) oc[i] = __builtin_fmaf(f, src[i], oc[i]);
+    }
+    if (a.parts > 1) {
+      if (out_ok) {
+        const int64_t slot = (((int64_t)c * a.entries + e) * a.H + h_out) * a.max_q_len + m_out;
+        float* dst = a.ws_o + slot * D + c8;
+        *reinterpret_cast<float4*>(dst) = make_float4(oc[0], oc[1], oc[2], oc[3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(oc[4], oc[5], oc[6], oc[7]);
+        if (c8 == 0) *reinterpret_cast<float2*>(a.ws_ml + 2 * slot) = make_float2(mc, lc);
+      }
+    } else {
+      attn_fold(Mr, Lr, Or, mc, lc, oc);
+    }
+    if (c + 1 < c_end) __syncthreads();  // every thread read the merge storage before reuse
   }
-  if (a.parts == 1) {
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    uint4 out;
-    out.x = pack_bf16x2(ov[0] * inv, ov[1] * inv);
-    out.y = pack_bf16x2(ov[2] * inv, ov[3] * inv);
-    out.z = pack_bf16x2(ov[4] * inv, ov[5] * inv);
-    out.w = pack_bf16x2(ov[6] * inv, ov[7] * inv);
-    *reinterpret_cast<uint4*>(a.o + (int64_t)h_out * a.so_h + (int64_t)(qs + m_out) * a.so_t + c8) =
-        out;
-  } else {
-    const int64_t slot =
-        (((int64_t)part * a.entries + e) * a.H + h_out) * a.max_q_len + m_out;
-    float* dst = a.ws_o + slot * D + c8;
-    *reinterpret_cast<float4*>(dst) = make_float4(ov[0], ov[1], ov[2], ov[3]);
-    *reinterpret_cast<float4*>(dst + 4) = make_float4(ov[4], ov[5], ov[6], ov[7]);
-    if (c8 == 0) *reinterpret_cast<float2*>(a.ws_ml + 2 * slot) = make_float2(M, L);
-  }
+  if (a.parts == 1 && out_ok)
+    *reinterpret_cast<uint4*>(a.o + (int64_t)h_out * a.so_h + (int64_t)(qs + m_out) * a.so_t +
+                              c8) = attn_out8(Lr, Or);
 }
 
-// Second pass of a split launch: one thread per (entry, head, query row, 8 columns) merges the
-// partitions the row's tile covered, in partition order.
+// Second pass of a split launch: one thread per (entry, head, query row, 8 columns) folds the
+// states of the chunks the row's tile covered, in chunk order, as the single-pass kernel does.
 template <int D>
 __global__ void __launch_bounds__(256)
 paged_attn_merge(PagedAttnArgs a) {
-  constexpr float NEG_INF = -__builtin_huge_valf();
   constexpr int C = D / 8;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t rows = (int64_t)a.entries * a.H * a.max_q_len;
@@ -302,58 +353,40 @@ paged_attn_merge(PagedAttnArgs a) {
   const int e = (int)(r / a.H);
   const int qlen = a.q_len[e];
   if (m >= qlen) return;
-  const int TQ = 16 / a.G;
-  const int end_n = attn_end(a.query_offset[e], qlen, a.context_len[e], m / TQ, TQ);
-  const int np = max(1, (end_n + a.chunk - 1) / a.chunk);
+  const int end_n = attn_end(a.query_offset[e], qlen, a.context_len[e], m / a.tq, a.tq);
+  const int np = attn_chunks(end_n);
   const int64_t stride = (int64_t)a.entries * a.H * a.max_q_len;
   const int64_t base = ((int64_t)e * a.H + h) * a.max_q_len + m;
-  float M = NEG_INF;
-  for (int p = 0; p < np; ++p) M = fmaxf(M, a.ws_ml[2 * (base + p * stride)]);
-  const float Mref = M == NEG_INF ? 0.0f : M;
-  float L = 0.0f, ov[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float M = -__builtin_huge_valf(), L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int p = 0; p < np; ++p) {
     const int64_t slot = base + p * stride;
-    const float f = exp2_fast(a.ws_ml[2 * slot] - Mref);
-    L += f * a.ws_ml[2 * slot + 1];
-    const float* src = a.ws_o + slot * D + c8;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ov[i] += f * src[i];
+    attn_fold(M, L, O, a.ws_ml[2 * slot], a.ws_ml[2 * slot + 1], a.ws_o + slot * D + c8);
   }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  uint4 out;
-  out.x = pack_bf16x2(ov[0] * inv, ov[1] * inv);
-  out.y = pack_bf16x2(ov[2] * inv, ov[3] * inv);
-  out.z = pack_bf16x2(ov[4] * inv, ov[5] * inv);
-  out.w = pack_bf16x2(ov[6] * inv, ov[7] * inv);
   *reinterpret_cast<uint4*>(a.o + (int64_t)h * a.so_h + (int64_t)(a.q_start[e] + m) * a.so_t + c8) =
-      out;
+      attn_out8(L, O);
 }
 
 // ---- host side -----------------------------------------------------------------------------
 
 struct AttnPlan {
-  int qtiles, parts, chunk;
+  int tq, qtiles, parts;
   int64_t ws_o_bytes, ws_bytes;
 };
 
-// Key partitions: one per (entry, K/V head, query tile) once those fill the CUs twice over;
-// otherwise the context bound (max_blocks x block_size) is cut so they do, in partitions of at
-// least 256 keys.
+// One workgroup per (entry, K/V head, query tile) item once those fill the CUs twice over;
+// otherwise, when the table's context bound (max_blocks x block_size) spans 2..kAttnMaxSplit
+// chunks, one workgroup per chunk (workgroups past a row's own chunks exit at once) and a second
+// pass that folds them. The choice depends on shapes only and changes no result.
 static AttnPlan attn_plan(int64_t entries, int64_t H, int64_t HKV, int64_t D, int64_t max_q_len,
                           int64_t max_ctx, int cus) {
   AttnPlan pl{};
-  const int64_t tq = 16 / (H / HKV);
-  pl.qtiles = (int)ceil_div(max_q_len, tq);
+  pl.tq = (int)(16 / (H / HKV));
+  pl.qtiles = (int)ceil_div(max_q_len, pl.tq);
   const int64_t items = entries * HKV * pl.qtiles;
-  int64_t parts = 1;
-  if (items > 0 && items < 2 * (int64_t)cus) {
-    parts = std::min<int64_t>(ceil_div(2 * (int64_t)cus, items), ceil_div(max_ctx, 256));
-    parts = std::max<int64_t>(parts, 1);
-  }
-  const int64_t chunk = ceil_div(ceil_div(std::max<int64_t>(max_ctx, 1), parts), kAttnPartKeys) *
-                        kAttnPartKeys;
-  pl.chunk = (int)chunk;
-  pl.parts = (int)ceil_div(std::max<int64_t>(max_ctx, 1), chunk);
+  const int64_t chunks = ceil_div(std::max<int64_t>(max_ctx, 1), kAttnChunk);
+  pl.parts = items > 0 && items < 2 * (int64_t)cus && chunks > 1 && chunks <= kAttnMaxSplit
+                 ? (int)chunks
+                 : 1;
   if (pl.parts > 1) {
     const int64_t slots = (int64_t)pl.parts * entries * H * max_q_len;
     pl.ws_o_bytes = slots * D * 4;
@@ -412,9 +445,9 @@ int launch_paged_attention(const uint16_t* q, int64_t sq_h, int64_t sq_t, const 
   const int64_t max_ctx = max_blocks * block_size;
   const AttnPlan pl = attn_plan(a.entries, a.H, a.HKV, 128, a.max_q_len, max_ctx, attn_cus());
   if (pl.ws_bytes > 0 && (ws_bytes < pl.ws_bytes || !ws)) return LSE_E_WORKSPACE;
+  a.tq = pl.tq;
   a.qtiles = pl.qtiles;
   a.parts = pl.parts;
-  a.chunk = pl.chunk;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.ws_o = pl.parts > 1 ? static_cast<float*>(ws) : nullptr;
   a.ws_ml = pl.parts > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + pl.ws_o_bytes) : nullptr;

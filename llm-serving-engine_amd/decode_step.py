@@ -18,10 +18,14 @@ applies o_proj (`attention_output`, model_runner.py:365-369).
     weight stream whose epilogue applies the MLP's SiLU-mul, so the (M, 28672) projection never
     leaves the kernel. Per-channel quantization of a row-stacked weight equals quantizing each
     part;
-  * "int8-torch": the same quantized weights, applied by an eager torch restatement of W8A16
-    (x and q·s in fp32, one fp32 matmul, bf16 out; gate/up as bf16 projections, then SiLU-mul,
-    as the reference's LlamaMLP rounds them) instead of the HIP kernels; it isolates the kernels
-    from the quantization itself. Test and measurement use only.
+  * "int8-torch": the same quantized weights, applied by an eager torch restatement of each
+    module's own arithmetic instead of the HIP kernels (`restate`: W8A16 s·Σ x·q in fp32, W8A8
+    per-token quantization, exact integer sums and (acc·sx)·s; gate/up as fp32 g and u with
+    silu(g)·u rounded once, as the fused kernel rounds it); it isolates the kernels from the
+    quantization itself. Test and measurement use only.
+With `trace` set to a list, every int8 projection of a step appends (layer, name, input,
+output), so each layer's kernels can be checked on the very input they saw (errors do not
+compound over layers).
 lm_head stays bf16 in both. Attention has two implementations: "torch", fp32 over a
 contiguous per-layer KV cache (the reference's `contiguous_attention` path,
 model_runner.py:400-418), the same arithmetic for both linear back ends so only the linears
@@ -86,6 +90,7 @@ class DecodeRunner:
         self.k_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
         self.v_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
         self.int8: list[dict[str, Int8Linear]] | None = None
+        self.trace: list | None = None
         self.backend = "bf16"
         self.attention = "torch"
         self.k_pool: list[torch.Tensor] | None = None
@@ -164,10 +169,12 @@ class DecodeRunner:
 
     def _lin(self, i: int, name: str, x: torch.Tensor) -> torch.Tensor:
         mod = self.int8[i][name]
-        if self.backend == "int8":
-            return mod(x)
-        w = mod.unpacked_qweight().float() * mod.scales[:, None]
-        return (x.float() @ w.t()).to(torch.bfloat16)
+        if self.backend != "int8":
+            return restate(mod, x)
+        y = mod(x)
+        if self.trace is not None:
+            self.trace.append((i, name, x, y))
+        return y
 
     def _qkv(self, i: int, normed: torch.Tensor):
         if self.backend == "bf16":
@@ -186,11 +193,7 @@ class DecodeRunner:
         mlp = self.layers[i].mlp
         if self.backend == "bf16":
             return mlp(x)
-        if self.backend == "int8":
-            return self._lin(i, "down", self.int8[i]["gate_up"](x))
-        gu = self._lin(i, "gate_up", x)
-        inter = gu.shape[-1] // 2
-        return self._lin(i, "down", mlp.act_fn(gu[..., :inter]) * gu[..., inter:])
+        return self._lin(i, "down", self._lin(i, "gate_up", x))
 
     # ---- the step -----------------------------------------------------------------------------
 
@@ -318,6 +321,32 @@ class SiluMul(nn.Module):
     def forward(self, gu: torch.Tensor) -> torch.Tensor:
         i = gu.shape[-1] // 2
         return self.act_fn(gu[..., :i]) * gu[..., i:]
+
+
+def _restate_f32(mode: str, x: torch.Tensor, q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """fp32 values an int8 projection rounds to bf16, restated in torch: W8A16 s[n]·Σ x·q (fp32
+    products and sums); W8A8 sx = amax/127 per token, xq = clamp(rne(x/sx)), acc = Σ xq·q exact
+    (an fp64 GEMM: integer sums below 2^53), then (acc·sx)·s."""
+    xf = x.float()
+    if mode == "int8":
+        return (xf @ q.float().t()) * s
+    amax = xf.abs().amax(-1, keepdim=True)
+    sx = torch.where(amax > 0, amax / 127.0, torch.ones_like(amax))
+    xq = torch.clamp(torch.round(xf / sx), -127, 127)
+    acc = (xq.double() @ q.double().t()).float()
+    return (acc * sx) * s
+
+
+def restate(mod: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """The eager torch restatement of an `Int8Linear` or `Int8GateUp` call on bf16 x (test and
+    measurement only): the module's mode and rounding points, without the HIP kernels. Gate/up:
+    h = bf16(silu(g)·u) from fp32 g and u, one rounding as in the fused kernel."""
+    q, s = mod.unpacked_qweight(), mod.scales
+    if isinstance(mod, Int8GateUp):
+        gu = _restate_f32(mod.mode, x, q, s)
+        inter = mod.intermediate_size
+        return (torch.nn.functional.silu(gu[..., :inter]) * gu[..., inter:]).to(torch.bfloat16)
+    return _restate_f32(mod.mode, x, q, s).to(torch.bfloat16)
 
 
 def _int8(weight: torch.Tensor, mode: str) -> Int8Linear:

@@ -352,7 +352,8 @@ def paged_attention_forward(
     q: (H, total_tokens, D) bf16. k_pool/v_pool: (num_blocks, block_size, H_KV, D) bf16, already
     holding this call's tokens. block_table (entries, max_blocks), context_len, query_offset,
     q_start, q_len (entries,): int32 on the device. max_q_len >= every q_len. Returns o like q.
-    Softmax scale 1/sqrt(D). D = 128 and H / H_KV in {1, 2, 4, 8, 16}."""
+    Softmax scale 1/sqrt(D). D = 128 and 1 <= H / H_KV <= 16 (24 query heads over 8 K/V
+    heads included)."""
     dev = _on_gpu(q, k_pool, v_pool, block_table, context_len, query_offset, q_start, q_len)
     _require(q.dim() == 3 and k_pool.dim() == 4 and v_pool.shape == k_pool.shape,
              "q must be (H, T, D), k_pool/v_pool (num_blocks, block_size, H_KV, D)")

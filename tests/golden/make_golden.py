@@ -4,7 +4,7 @@ The reference ships no golden vectors for the int8 Linear path (its int8 switch 
 src/llm_serving_engine/model/model_runner.py:45-46), so these fixtures are the oracle's own
 outputs on small seeded inputs, frozen so that any later change to the oracle's numerics or to
 the seeded input generator is caught (tests/test_oracle.py), and so the GPU tests have fixed
-vectors to match (tests/test_gpu_golden.py).
+vectors to match (tests/test_gpu_golden.py replays them through the HIP kernels).
 
     python tests/golden/make_golden.py
 """

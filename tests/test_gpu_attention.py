@@ -77,26 +77,105 @@ def test_mixed_prefill_chunks_and_decode(pkg, dev):
     _check(pkg, dev, _case(2, entries, block_size=7), "mixed")
 
 
-@pytest.mark.parametrize("h,h_kv", [(8, 8), (16, 8), (32, 4), (32, 2)])
+@pytest.mark.parametrize("h,h_kv", [(8, 8), (16, 8), (32, 4), (32, 2), (24, 8), (40, 8), (96, 8)])
 def test_head_groupings(pkg, dev, h, h_kv):
-    """MHA (1 query head per K/V head) up to 16 query heads per K/V head."""
-    entries = [(5, 10, 15), (1, 40, 41), (20, 0, 20)]
-    _check(pkg, dev, _case(3 + h_kv, entries, h=h, h_kv=h_kv), f"H={h} H_KV={h_kv}")
+    """MHA (1 query head per K/V head) up to 16 query heads per K/V head, including groups that
+    do not divide the 16-row tile: 24 over 8 (the reference's default model,
+    unsloth/Llama-3.2-3B-Instruct, config.py:29), 5 and 12 per K/V head."""
+    entries = [(5, 10, 15), (1, 40, 41), (20, 0, 20), (7, 600, 607)]
+    _check(pkg, dev, _case(3 + h_kv + h, entries, h=h, h_kv=h_kv), f"H={h} H_KV={h_kv}")
 
 
 @pytest.mark.parametrize("ctx", [300, 4096, 9000])
-def test_long_contexts_split_into_partitions(pkg, dev, ctx):
-    """Few (entry, head) items over long contexts take the split path: partitions merged by a
-    second pass. Deterministic: two calls agree bitwise."""
+def test_long_contexts_split_into_chunks(pkg, dev, ctx):
+    """Few (entry, head) items over contexts longer than one 512-key chunk take the split path:
+    one workgroup per chunk, folded by a second pass. Deterministic: two calls agree bitwise."""
     c = _case(10 + ctx, [(1, ctx - 1, ctx), (3, ctx - 3, ctx)], block_size=32)
     nbytes = pkg.library().lse_paged_attention_workspace_bytes(
         2, 32, 8, 128, c["max_q_len"], c["table"].shape[1], c["bs"])
-    assert nbytes > 0, "expected the split path"
+    assert (nbytes > 0) == (ctx > 512), "the split path serves contexts of two chunks or more"
     first = _check(pkg, dev, c, f"ctx={ctx}")
     np.testing.assert_array_equal(_run(pkg, dev, c), first)
 
 
-def test_graph_bucket_larger_than_the_batch(pkg, dev):
+def _widened(c, bucket, pool_wide=True, scratch_fill=True):
+    """The reference's graphed-decode call shape for case c (decode_graph.py:87-212): `bucket`
+    entries whose rows past the real ones are padding (q_len 0, context 0, table on a scratch
+    block), and a block table as wide as the whole pool (`_alloc`, num_blocks = the scratch id)."""
+    e = len(c["ql"])
+    nblocks = c["kp"].shape[0]
+    width = nblocks if pool_wide else c["table"].shape[1]
+    table = np.full((bucket, width), nblocks - 1 if scratch_fill else 0, np.int32)
+    table[:e, :c["table"].shape[1]] = c["table"]
+    pad = lambda a: np.concatenate([a, np.zeros(bucket - e, np.int32)])  # noqa: E731
+    w = dict(c)
+    w.update(table=table, ctx=pad(c["ctx"]), qo=pad(c["qo"]), ql=pad(c["ql"]),
+             qs=np.concatenate([c["qs"], np.full(bucket - e, int(c["ql"].sum()), np.int32)]))
+    return w
+
+
+def test_rows_do_not_depend_on_batch_or_table_width(pkg, dev):
+    """The reference's Triton kernel never splits a row over keys (grid (cdiv(max_q_len, BLOCK_M),
+    entries * H), kernels/flash_attention.py:311), so a row's result does not depend on the rest of
+    the call: its graphed decode (a bucket of entries padded with q_len = 0 rows, a table as wide
+    as the pool, decode_graph.py:97,149) and its eager path (the batch's own entries and table
+    width, model_runner.py:268-280) give the same tokens (tests/test_decode_graph.py:53-59). The
+    HIP kernel keeps that bitwise: five decode rows over 1 to 2100 keys run as the eager call (40
+    items: one workgroup per 512-key chunk, folded by the second pass), as a 64-entry graph bucket
+    over a pool-wide table (512 items: chunks folded inside one workgroup), with a larger
+    max_q_len, and reordered inside another batch."""
+    ctxs = [2100, 1, 513, 300, 1030]
+    c = _case(60, [(1, n - 1, n) for n in ctxs], spare_blocks=40)
+    base = _check(pkg, dev, c, "eager shape")
+    lib = pkg.library()
+    assert lib.lse_paged_attention_workspace_bytes(5, 32, 8, 128, 1, c["table"].shape[1], 16) > 0
+    g = _widened(c, 64)
+    assert lib.lse_paged_attention_workspace_bytes(64, 32, 8, 128, 1, g["table"].shape[1], 16) == 0
+    o = _run(pkg, dev, g)
+    np.testing.assert_array_equal(o[:, :len(ctxs)], base, err_msg="graph bucket, pool-wide table")
+    g8 = dict(g, max_q_len=8)
+    np.testing.assert_array_equal(_run(pkg, dev, g8)[:, :len(ctxs)], base, err_msg="max_q_len 8")
+    w = _widened(c, 9, pool_wide=True, scratch_fill=False)
+    np.testing.assert_array_equal(_run(pkg, dev, w)[:, :len(ctxs)], base, err_msg="bucket 9")
+    # The same rows reversed, after a prefill chunk of another entry, in one call.
+    order = list(reversed(range(len(ctxs))))
+    other_blocks = list(range(c["kp"].shape[0] - 40, c["kp"].shape[0] - 38))
+    table = np.zeros((len(ctxs) + 1, c["table"].shape[1]), np.int32)
+    table[0, :2] = other_blocks
+    for i, src in enumerate(order):
+        table[i + 1] = c["table"][src]
+    mixed = dict(c, table=table,
+                 ctx=np.array([20] + [c["ctx"][s] for s in order], np.int32),
+                 qo=np.array([0] + [c["qo"][s] for s in order], np.int32),
+                 ql=np.array([20] + [1] * len(ctxs), np.int32),
+                 qs=np.array([0] + list(range(20, 20 + len(ctxs))), np.int32), max_q_len=20)
+    q = np.zeros((c["q"].shape[0], 20 + len(ctxs), 128), np.uint16)
+    q[:, :20] = c["q"][:, :1]
+    for i, src in enumerate(order):
+        q[:, 20 + i] = c["q"][:, src]
+    mixed["q"] = q
+    om = _check(pkg, dev, mixed, "mixed batch")
+    for i, src in enumerate(order):
+        np.testing.assert_array_equal(om[:, 20 + i], base[:, src], err_msg=f"mixed row {src}")
+
+
+def test_contexts_beyond_the_split_limit(pkg, dev):
+    """A table spanning more than 64 chunks (32768 keys) runs every item in one workgroup; the
+    rows still equal the split launch of a narrower table bitwise."""
+    c = _case(70, [(1, 2999, 3000), (2, 998, 1000)], block_size=16)
+    base = _run(pkg, dev, c)
+    wide = dict(c)
+    width = 2100  # 33600 keys: 66 chunks, no split
+    lib = pkg.library()
+    assert lib.lse_paged_attention_workspace_bytes(2, 32, 8, 128, 2, width, 16) == 0
+    assert lib.lse_paged_attention_workspace_bytes(2, 32, 8, 128, 2, c["table"].shape[1], 16) > 0
+    table = np.zeros((2, width), np.int32)
+    table[:, :c["table"].shape[1]] = c["table"]
+    wide["table"] = table
+    np.testing.assert_array_equal(_run(pkg, dev, wide), base)
+
+
+def test_graph_bucket_larger_than_the_max_q_len(pkg, dev):
     """max_q_len above every q_len (a graphed decode's bucket) changes nothing."""
     c = _case(20, [(1, 9, 10), (1, 99, 100)])
     base = _run(pkg, dev, c)

@@ -42,6 +42,35 @@ def test_round_trip_is_bit_identical(pkg, dev, tmp_path, mode):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("mode", ["int8", "w8a8"])
+def test_round_trip_keeps_projection_biases(pkg, dev, tmp_path, mode):
+    """attention_bias and mlp_bias configs (transformers modeling_llama.py:169-171, 231-241):
+    the biases are stored beside each projection's int8 weight and restored, the MLP stays
+    unfused (the fused kernel takes bias-free projections), and logits are bit-identical."""
+    from safetensors import safe_open
+
+    base = _llama(dev, 7, attention_bias=True, mlp_bias=True)
+    with torch.no_grad():
+        for name, p in base.named_parameters():
+            if name.endswith(".bias"):
+                p.normal_(0.0, 0.5)
+    model = pkg.quantize_model_(base, mode)
+    ids = torch.randint(0, 96, (1, 9), device=dev)
+    with torch.no_grad():
+        ref = model(ids).logits
+    path = pkg.save_int8_checkpoint(model, tmp_path / "b.safetensors")
+    with safe_open(str(path), "pt") as f:
+        biases = [k for k in f.keys() if k.endswith(".bias")]
+    assert len(biases) == 2 * 7, biases  # q, k, v, o, gate, up, down in each of 2 layers
+    loaded = pkg.load_int8_checkpoint(path, dev)
+    for layer in loaded.model.layers:
+        assert layer.self_attn.o_proj.bias is not None
+        assert isinstance(layer.mlp.down_proj, pkg.Int8Linear) and layer.mlp.down_proj.bias is not None
+    with torch.no_grad():
+        got = loaded(ids).logits
+    assert torch.equal(got, ref)
+
+
 def test_unfused_model_saves_the_same_weights(pkg, dev, tmp_path):
     """A model quantized without MLP fusion stores the same tensors; it reloads fused."""
     from safetensors import safe_open

@@ -233,9 +233,37 @@ def test_llama_decode_shapes_full_size(pkg, dev, k, n):
         assert ok, f"M={m} K={k} N={n}: {msg}"
 
 
+def check_rows_in_chunks(y, golden, rows=1024):
+    """The oracle's W8A16 rule over blocks of `rows` rows (each against its own max|golden|, no
+    looser than one check of the whole matrix): y bf16 and golden fp64 on the GPU, compared on
+    the host a block at a time so a (8192, 28672) product never sits in host memory at once."""
+    for r0 in range(0, y.shape[0], rows):
+        ok, msg = ora.within_tolerance(bf16_bits(y[r0:r0 + rows]),
+                                       golden[r0:r0 + rows].cpu().numpy())
+        if not ok:
+            return False, f"rows {r0}..{r0 + rows}: {msg}"
+    return True, "ok"
+
+
+@pytest.mark.parametrize("k,n", LLAMA_SHAPES)
+def test_llama_prefill_shapes_at_8192_tokens(pkg, dev, k, n):
+    """Config 2 at its largest size, M = 8192, every Llama-3-8B shape, against the fp64 product of
+    the same bf16 activations and dequantized weights on the GPU."""
+    gen = torch.Generator(device="cpu").manual_seed(2500 + k + n)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
+    q, s = pkg.ops.quantize_weight_per_channel(w)
+    del w
+    qp = pkg.ops.pack_weight(q)
+    x = torch.randn(8192, k, generator=gen).to(torch.bfloat16).to(dev)
+    y = pkg.ops.w8a16_linear(x, qp, s, algo=PREFILL)
+    golden = (x.double() @ q.double().t()) * s.double()[None, :]
+    ok, msg = check_rows_in_chunks(y, golden)
+    assert ok, f"M=8192 K={k} N={n}: {msg}"
+
+
 @pytest.mark.parametrize("k,n", LLAMA_SHAPES)
 def test_llama_prefill_shapes_full_size(pkg, dev, k, n):
-    """Config 2 at M=512 and 2048 (8192 is covered by the bench) vs torch fp32 on the GPU."""
+    """Config 2 at M=512 and 2048 vs torch fp32 on the GPU (8192 in the test above)."""
     gen = torch.Generator(device="cpu").manual_seed(2000 + k + n)
     w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
     q, s = pkg.ops.quantize_weight_per_channel(w)

@@ -99,6 +99,30 @@ def test_llama_shapes_full_size(pkg, dev, k, n):
         np.testing.assert_array_equal(bf16_bits(y), y_ref)
 
 
+@pytest.mark.parametrize("k,n", LLAMA_SHAPES)
+def test_llama_shapes_at_4096_tokens(pkg, dev, k, n):
+    """Config 3 at its largest size, M = 4096, every Llama-3-8B shape, with the outlier columns:
+    the quantizer against the oracle, the accumulators exactly against an fp64 GEMM on the GPU
+    (integer partial sums below 2^53 are exact in fp64, in any order), the epilogue against the
+    oracle's, a block of rows at a time."""
+    x_bits, w = ora.seeded_inputs(3500 + k + n, 4096, n, k, outliers=True)
+    q, s = pkg.ops.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    del w
+    qp = pkg.ops.pack_weight(q)
+    xq, sx = pkg.ops.quantize_act_per_token(to_bf16_tensor(x_bits, dev))
+    y, acc = pkg.ops.w8a8_gemm(xq, sx, qp, s, True)
+    xq_ref, sx_ref = ora.quantize_act_per_token(x_bits)
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+    np.testing.assert_array_equal(sx.cpu().numpy(), sx_ref)
+    exact = (xq.double() @ q.double().t()).round().to(torch.int64)
+    assert torch.equal(acc.to(torch.int64), exact), f"M=4096 K={k} N={n}"
+    del exact
+    s_host = s.cpu().numpy()
+    for r0 in range(0, 4096, 1024):
+        y_ref = ora.w8a8_epilogue(acc[r0:r0 + 1024].cpu().numpy(), sx_ref[r0:r0 + 1024], s_host)
+        np.testing.assert_array_equal(bf16_bits(y[r0:r0 + 1024]), y_ref, err_msg=f"rows {r0}..")
+
+
 def test_acc_only_and_y_only(pkg, dev):
     x_bits, w = ora.seeded_inputs(61, 20, 64, 256, outliers=True)
     q, s = ora.quantize_weight_per_channel(w)

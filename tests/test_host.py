@@ -186,3 +186,38 @@ def test_checkpoint_reader_refuses_other_files(pkg, tmp_path):
               metadata={"format": "lse-int8", "format_version": "9"})
     with pytest.raises(RuntimeError, match="format_version"):
         checkpoint.read_metadata(tmp_path / "v9.safetensors")
+
+
+def test_checkpoint_refuses_architectures_it_cannot_rebuild(pkg, tmp_path):
+    """The loader rebuilds LlamaForCausalLM only: saving or loading another model type (a Qwen2
+    config the reference's AutoModelForCausalLM would load, say) raises instead of silently
+    dropping what the Llama skeleton lacks."""
+    import json
+
+    from safetensors.torch import save_file
+
+    from llm_serving_engine_amd import checkpoint
+
+    model = _cpu_int8_llama(pkg, True)
+    model.config.model_type = "qwen2"
+    with pytest.raises(RuntimeError, match="rebuild"):
+        pkg.save_int8_checkpoint(model, tmp_path / "q.safetensors")
+    save_file({"x": torch.zeros(2)}, str(tmp_path / "q2.safetensors"),
+              metadata={"format": "lse-int8", "format_version": "1", "mode": "int8",
+                        "config": json.dumps({"model_type": "qwen2"})})
+    with pytest.raises(RuntimeError, match="rebuild"):
+        checkpoint.load_int8_checkpoint(tmp_path / "q2.safetensors", "cpu")
+
+
+def test_checkpoint_stores_projection_biases(pkg, tmp_path):
+    from safetensors import safe_open
+
+    model = _cpu_int8_llama(pkg, False)
+    lin = pkg.Int8Linear(32, 32, "int8", bias=True, device="cpu")
+    lin.bias.fill_(0.25)
+    model.model.layers[0].self_attn.o_proj = lin
+    path = pkg.save_int8_checkpoint(model, tmp_path / "b.safetensors")
+    with safe_open(str(path), "pt") as f:
+        b = f.get_tensor("model.layers.0.self_attn.o_proj.bias")
+        assert b.dtype == torch.bfloat16 and torch.all(b == 0.25)
+        assert "model.layers.1.self_attn.o_proj.bias" not in set(f.keys())
