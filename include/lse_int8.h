@@ -52,6 +52,8 @@ enum lse_status {
   LSE_E_RANGE = -4,       /* K too large for exact int32 accumulation, or a size beyond int32 grids */
   LSE_E_ALGO = -5,        /* unknown algorithm id, or one that cannot run this shape */
   LSE_E_WORKSPACE = -6,   /* workspace NULL or smaller than lse_workspace_bytes for the call */
+  LSE_E_SCRATCH = -7,     /* lse_w8a16_gemm_noalloc: the call needs more workspace than the
+                             library's static scratch (LSE_NOALLOC_SCRATCH_BYTES) holds */
 };
 
 /* Arithmetic mode, for lse_workspace_bytes. */
@@ -74,9 +76,11 @@ enum lse_query_key {
   LSE_Q_DECODE_MAX_M = 2, /* largest M the decode kernel takes */
   LSE_Q_MAX_K = 3,        /* largest K with exact int32 W8A8 accumulation */
   LSE_Q_GFX_ARCH = 4,     /* the code-object target, e.g. 950 */
+  LSE_Q_NOALLOC_SCRATCH = 5, /* bytes of the static scratch lse_w8a16_gemm_noalloc works in */
 };
 
-#define LSE_ABI_VERSION 8
+#define LSE_ABI_VERSION 9
+#define LSE_NOALLOC_SCRATCH_BYTES (16 << 20)
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -126,6 +130,21 @@ int64_t lse_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K);
 int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
                    int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
                    int64_t workspace_bytes, void* stream);
+
+/*
+ * lse_w8a16_gemm without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls
+ * no hipMalloc, hipFree or allocating routine: the workspace lse_w8a16_gemm would take lives in a
+ * static device array of LSE_NOALLOC_SCRATCH_BYTES (16 MiB) that each device the library runs on
+ * holds until the process ends, its device address looked up on the device's first call. Same
+ * kernels, so y is bit-identical to lse_w8a16_gemm's. Calls that overlap on one device (two
+ * streams at once) share that array and race; calls in stream order do not. Returns
+ * LSE_E_SCRATCH when lse_workspace_bytes(LSE_MODE_W8A16, M, N, K) exceeds the array.
+ * Replaces: nothing in the reference (it has no such caller); an addition for callers that
+ * cannot allocate.
+ */
+int lse_w8a16_gemm_noalloc(const void* x, int64_t ldx, const int8_t* qp, const float* s,
+                           void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* lse_w8a16_gemm with the kernel family chosen by the caller (enum lse_algo); used to test
  * the decode and prefill kernels on identical inputs. Same contract otherwise. */

@@ -23,6 +23,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lse_pack_weight": (_INT, [_P, _I64, _I64, _P, _P]),
     "lse_workspace_bytes": (_I64, [_INT, _I64, _I64, _I64]),
     "lse_w8a16_gemm": (_INT, [_P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "lse_w8a16_gemm_noalloc": (_INT, [_P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "lse_w8a16_gemm_algo": (
         _INT, [_P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P, _I64, _P]),
     "lse_quantize_act_per_token": (_INT, [_P, _I64, _P, _P, _I64, _I64, _P]),
@@ -49,9 +50,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 LSE_OK = 0
 ALGO_AUTO, ALGO_DECODE, ALGO_PREFILL = 0, 1, 2
 MODE_W8A16, MODE_W8A8 = 0, 1
-E_WORKSPACE = -6
+E_WORKSPACE, E_SCRATCH = -6, -7
 Q_ABI_VERSION, Q_K_ALIGN, Q_DECODE_MAX_M, Q_MAX_K, Q_GFX_ARCH = 0, 1, 2, 3, 4
-ABI_VERSION = 8
+Q_NOALLOC_SCRATCH = 5
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -3,7 +3,6 @@
 // launched; a launch failure returns the hipError_t.
 #include <algorithm>
 #include <mutex>
-#include <vector>
 
 #include "lse_common.h"
 
@@ -67,19 +66,25 @@ int launch_paged_attention(const uint16_t* q, int64_t sq_h, int64_t sq_t, const 
 namespace lse {
 
 int persistent_blocks(const void* kernel, int threads, size_t dyn_lds) {
+  // A fixed table, so no launch path allocates (host or device); past its size the occupancy
+  // query simply runs again.
   struct Entry {
     int device;
     const void* kernel;
     size_t dyn_lds;
     int blocks;
   };
+  constexpr int kEntries = 512;
   static std::mutex mu;
-  static std::vector<Entry> cache;
+  static Entry cache[kEntries];
+  static int used = 0;
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return 1;
   std::lock_guard<std::mutex> lock(mu);
-  for (const Entry& e : cache)
+  for (int i = 0; i < used; ++i) {
+    const Entry& e = cache[i];
     if (e.device == device && e.kernel == kernel && e.dyn_lds == dyn_lds) return e.blocks;
+  }
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, dyn_lds) !=
@@ -88,7 +93,7 @@ int persistent_blocks(const void* kernel, int threads, size_t dyn_lds) {
     return 256;
   }
   const int blocks = std::max(1, cus * std::max(1, per_cu));
-  cache.push_back({device, kernel, dyn_lds, blocks});
+  if (used < kEntries) cache[used++] = Entry{device, kernel, dyn_lds, blocks};
   return blocks;
 }
 
@@ -460,6 +465,7 @@ int64_t lse_query(int key) {
     case LSE_Q_DECODE_MAX_M: return LSE_DECODE_MAX_M;
     case LSE_Q_MAX_K: return LSE_MAX_K;
     case LSE_Q_GFX_ARCH: return 950;
+    case LSE_Q_NOALLOC_SCRATCH: return LSE_NOALLOC_SCRATCH_BYTES;
     default: return -1;
   }
 }
@@ -473,6 +479,9 @@ const char* lse_status_string(int status) {
     case LSE_E_RANGE: return "size out of range (int32 accumulation or grid limits)";
     case LSE_E_ALGO: return "unknown algorithm, or one that cannot run this shape";
     case LSE_E_WORKSPACE: return "workspace missing, misaligned or smaller than lse_workspace_bytes";
+    case LSE_E_SCRATCH:
+      return "the call needs more workspace than lse_w8a16_gemm_noalloc's static scratch "
+             "(LSE_NOALLOC_SCRATCH_BYTES) holds";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
   }
 }

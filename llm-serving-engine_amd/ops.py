@@ -36,6 +36,7 @@ __all__ = [
     "w8a8_linear",
     "w8a16_glu",
     "w8a16_linear",
+    "w8a16_linear_noalloc",
     "workspace",
 ]
 
@@ -198,6 +199,28 @@ def w8a16_linear(
         "lse_w8a16_gemm",
     )
     return y.view(*x.shape[:-1], n)
+
+
+def w8a16_linear_noalloc(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor,
+                         out: torch.Tensor) -> torch.Tensor:
+    """`w8a16_linear` into a caller-given `out` (M, N) bf16 through `lse_w8a16_gemm_noalloc`:
+    nothing is allocated (the decode kernel's split-K partial sums live in the library's static
+    per-device scratch). x must already be (M, K) with a contiguous last dim."""
+    dev = _on_gpu(x, qp, scales, out)
+    _require(x.dtype == torch.bfloat16 and out.dtype == torch.bfloat16, "bf16 x and out expected")
+    _require(scales.dtype == torch.float32 and scales.dim() == 1, "scales must be fp32 (N,)")
+    _require(x.dim() == 2 and x.stride(-1) == 1, "x must be (M, K) with a contiguous last dim")
+    n, (m, k) = scales.shape[0], x.shape
+    _check_packed(qp, n, k)
+    _require(out.dim() == 2 and tuple(out.shape) == (m, n) and out.stride(-1) == 1,
+             f"out must be ({m}, {n}) with a contiguous last dim")
+    _lib.check(
+        _lib.library().lse_w8a16_gemm_noalloc(
+            x.data_ptr(), x.stride(0) if m > 1 else k, qp.data_ptr(), scales.data_ptr(),
+            out.data_ptr(), out.stride(0) if m > 1 else n, m, n, k, _stream(dev)),
+        "lse_w8a16_gemm_noalloc",
+    )
+    return out
 
 
 def quantize_act_per_token(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
