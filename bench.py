@@ -198,6 +198,13 @@ def bench_decode(pkg, dev, steps: int, warmup: int, gen) -> dict:
         t = time_region(graph_of(sub).replay, steps, 1) / (steps * len(sub))
         by_shape[f"kv_proj_M{m}"] = {
             "us": round(t * 1e6, 2), "gbps": round(decode_bytes(m, k, n) / t / 1e9, 1)}
+    # The attention projections as the drop-in runs them: q_proj (the o_proj shape) + k_proj +
+    # v_proj as three launches, against the grouped q/k/v (QKVGroup: one stacked qkv launch).
+    qkv_drop_in = {}
+    for m in DECODE_MS:
+        sep = by_shape[f"o_proj_M{m}"]["us"] + 2 * by_shape[f"kv_proj_M{m}"]["us"]
+        qkv_drop_in[str(m)] = {"separate_us": round(sep, 2),
+                               "grouped_us": by_shape[f"qkv_M{m}"]["us"]}
     return {
         "seconds_per_step": per_step,
         "bytes_per_step": total_bytes,
@@ -205,6 +212,7 @@ def bench_decode(pkg, dev, steps: int, warmup: int, gen) -> dict:
         "gbps": total_bytes / per_step / 1e9,
         "by_m_gbps": by_m,
         "by_shape": by_shape,
+        "qkv_drop_in": qkv_drop_in,
     }
 
 
@@ -1112,6 +1120,7 @@ def main() -> None:
         "cpu_int8_restatements": cpu_int8,
         "decode_by_m_gbps": dec["by_m_gbps"],
         "decode_by_shape": dec["by_shape"],
+        "decode_attention_projections_drop_in": dec["qkv_drop_in"],
         **secondary,
     }
     print(json.dumps(out))

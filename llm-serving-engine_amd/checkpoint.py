@@ -29,7 +29,7 @@ import torch
 from torch import nn
 
 from . import ops
-from .int8_linear import Int8GateUp, Int8GluMLP, Int8Linear, Int8RMSNormQuant
+from .int8_linear import Int8GateUp, Int8GluMLP, Int8Linear, Int8RMSNormQuant, group_qkv
 
 FORMAT = "lse-int8"
 MODEL_TYPES = ("llama",)  # architectures the loader rebuilds (LlamaForCausalLM)
@@ -171,6 +171,7 @@ def load_int8_checkpoint(path: str | Path, device: torch.device | str = "cuda") 
             prefix = f"model.layers.{i}"
             for name in ATTENTION:
                 setattr(layer.self_attn, name, linear(f"{prefix}.self_attn.{name}"))
+            group_qkv(layer.self_attn)  # as quantize_model_ leaves them by default
             if fused:
                 qg, sg = load_q(f"{prefix}.mlp.gate_proj")
                 qu, su = load_q(f"{prefix}.mlp.up_proj")

@@ -111,13 +111,11 @@ class Int8Linear(nn.Module):
         return ops.unpack_weight(self.qweight, self.out_features, self.in_features)
 
     def forward(self, x: torch.Tensor | QuantizedRows) -> torch.Tensor:
-        if _w8a8_input(self, x):
-            y, _ = ops.w8a8_gemm(x.xq, x.sx, self.qweight, self.scales)
-            y = y.view(*x.shape[:-1], self.out_features)
-        elif self.mode == "int8":
-            y = ops.w8a16_linear(x, self.qweight, self.scales)
+        group = self.__dict__.get("_qkv_group")
+        if group is not None:
+            y = group.columns(self, x)
         else:
-            y = ops.w8a8_linear(x, self.qweight, self.scales)
+            y = _int8_product(self.mode, x, self.qweight, self.scales, self.out_features)
         return y if self.bias is None else y + self.bias
 
     def extra_repr(self) -> str:
@@ -125,6 +123,94 @@ class Int8Linear(nn.Module):
             f"in_features={self.in_features}, out_features={self.out_features}, "
             f"mode={self.mode}, bias={self.bias is not None}"
         )
+
+
+def _int8_product(mode: str, x: torch.Tensor | QuantizedRows, qweight: torch.Tensor,
+                  scales: torch.Tensor, n: int) -> torch.Tensor:
+    """x (..., K) times a packed int8 weight of n rows, without bias, in `mode`."""
+    if isinstance(x, QuantizedRows):
+        if mode != "w8a8":
+            raise RuntimeError("pre-quantized rows reach a weight-only (int8) projection")
+        y, _ = ops.w8a8_gemm(x.xq, x.sx, qweight, scales)
+        return y.view(*x.shape[:-1], n)
+    if mode == "int8":
+        return ops.w8a16_linear(x, qweight, scales)
+    return ops.w8a8_linear(x, qweight, scales)
+
+
+class QKVGroup:
+    """One attention layer's q, k and v projections as one int8 GEMM over their stacked weights.
+
+    The reference calls the three as separate modules on the same input, one after another
+    (`_project_qkv`, src/llm_serving_engine/model/model_runner.py:322-324; HF LlamaAttention,
+    modeling_llama.py:254-256). Separately they are three weight streams of which two (the
+    (K, 1024) k and v of Llama-3-8B) are too small to fill the GPU; stacked they are one stream
+    of (K, 6144). The modules keep their own buffers, which are views of the stacked packed weight
+    (row tiles of the tile layout, so each slice is itself a packed weight) and of the stacked
+    scales. The first of the three calls on an input computes all columns; the others return
+    their columns of that result, as long as they see the very same input object, unmodified
+    (same tensor version), and the result is dropped once all three have taken their columns.
+    Any other call computes the stacked product afresh. Each module's output is a column view of
+    the (..., Nq + Nk + Nv) product, bit-identical to what the stacked weight gives for those
+    columns."""
+
+    def __init__(self, qweight: torch.Tensor, scales: torch.Tensor, mode: str,
+                 members: list[Int8Linear]) -> None:
+        self.qweight, self.scales, self.mode = qweight, scales, mode
+        self.n = int(scales.shape[0])
+        self.offsets: dict[int, tuple[int, int]] = {}
+        at = 0
+        for mod in members:
+            self.offsets[id(mod)] = (at, at + mod.out_features)
+            at += mod.out_features
+        self._input = None
+        self._version = -1
+        self._out: torch.Tensor | None = None
+        self._pending: set[int] = set()
+
+    @staticmethod
+    def _version_of(x) -> int:
+        return (x.xq if isinstance(x, QuantizedRows) else x)._version
+
+    def columns(self, mod: Int8Linear, x) -> torch.Tensor:
+        key = id(mod)
+        hit = (self._out is not None and x is self._input and key in self._pending
+               and self._version_of(x) == self._version)
+        if not hit:
+            self._out = _int8_product(self.mode, x, self.qweight, self.scales, self.n)
+            self._input, self._version = x, self._version_of(x)
+            self._pending = set(self.offsets)
+        out = self._out
+        self._pending.discard(key)
+        if not self._pending:  # all three served: release the input and the product
+            self._out = self._input = None
+        a, b = self.offsets[key]
+        return out[..., a:b]
+
+
+def group_qkv(attn: nn.Module) -> QKVGroup | None:
+    """Makes `attn`'s q_proj, k_proj and v_proj (Int8Linear, one mode, one input width, row counts
+    multiples of 16, biases all present or all absent) views of one stacked packed weight run by
+    a `QKVGroup`. Returns the group, or None when they do not qualify (they then stay separate)."""
+    mods = [getattr(attn, n, None) for n in ("q_proj", "k_proj", "v_proj")]
+    if not all(isinstance(m, Int8Linear) for m in mods):
+        return None
+    if (len({m.mode for m in mods}) != 1 or len({m.in_features for m in mods}) != 1
+            or any(m.out_features % 16 for m in mods)
+            or len({m.bias is None for m in mods}) != 1):
+        return None
+    qweight = torch.cat([m.qweight for m in mods])  # row tiles stack: still the tile layout
+    scales = torch.cat([m.scales for m in mods])
+    at = 0
+    for m in mods:
+        rb = m.out_features // 16
+        m._buffers["qweight"] = qweight[at // 16:at // 16 + rb]
+        m._buffers["scales"] = scales[at:at + m.out_features]
+        at += m.out_features
+    group = QKVGroup(qweight, scales, mods[0].mode, mods)
+    for m in mods:
+        m.__dict__["_qkv_group"] = group
+    return group
 
 
 def check_linear_supported(linear: nn.Linear) -> None:

@@ -16,7 +16,8 @@ import gc
 import torch
 from torch import nn
 
-from .int8_linear import MODES, Int8GluMLP, Int8Linear, Int8RMSNormQuant, fusable_mlp
+from .int8_linear import (MODES, Int8GluMLP, Int8Linear, Int8RMSNormQuant, fusable_mlp,
+                          group_qkv)
 
 ATTENTION_PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj")
 MLP_PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
@@ -39,13 +40,15 @@ def check_int8_support(model: nn.Module) -> None:
 
 @torch.no_grad()
 def quantize_model_(model: nn.Module, mode: str = "int8", fuse_mlp: bool = True,
-                    fuse_norm: bool | None = None) -> nn.Module:
+                    fuse_norm: bool | None = None, fuse_qkv: bool = True) -> nn.Module:
     """Replaces q/k/v/o of every decoder layer by `Int8Linear` (per-channel int8 weights
     quantized on the GPU) and its MLP by `Int8GluMLP` (fused gate/up + SiLU-mul, then down), or,
-    with `fuse_mlp=False` or an MLP of another form, gate/up/down by `Int8Linear` each. In the
-    W8A8 mode (`fuse_norm`, default on for "w8a8") the layer's two RMSNorms become
-    `Int8RMSNormQuant`, which quantizes the normed rows once for all their projections. Returns
-    the same model object."""
+    with `fuse_mlp=False` or an MLP of another form, gate/up/down by `Int8Linear` each. With
+    `fuse_qkv` the layer's q, k and v projections share one stacked weight (`QKVGroup`): the
+    three module calls the runner makes on one input run as one GEMM. In the W8A8 mode
+    (`fuse_norm`, default on for "w8a8") the layer's two RMSNorms become `Int8RMSNormQuant`,
+    which quantizes the normed rows once for all their projections. Returns the same model
+    object."""
     if mode not in MODES:
         raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
     if fuse_norm is None:
@@ -65,6 +68,8 @@ def quantize_model_(model: nn.Module, mode: str = "int8", fuse_mlp: bool = True,
                 if isinstance(linear, nn.Linear):
                     setattr(parent, name, Int8Linear.from_linear(linear, mode))
                     del linear
+        if fuse_qkv:
+            group_qkv(layer.self_attn)
         if fuse_norm:
             for name in ("input_layernorm", "post_attention_layernorm"):
                 norm = getattr(layer, name)

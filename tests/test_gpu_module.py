@@ -121,3 +121,100 @@ def test_load_time_refusals(pkg, dev):
     fp16_model = nn.Module()
     with pytest.raises(RuntimeError, match="Llama"):
         pkg.quantize_model_(fp16_model)
+
+
+def _attention_projections(pkg, dev, mode, bias=False, seed=30):
+    """q (256 -> 256), k and v (256 -> 64) of one attention layer, as Int8Linear."""
+    attn = nn.Module()
+    for i, (name, n) in enumerate((("q_proj", 256), ("k_proj", 64), ("v_proj", 64))):
+        setattr(attn, name, pkg.Int8Linear.from_linear(_linear(dev, 256, n, seed + i, bias), mode))
+    return attn
+
+
+@pytest.mark.parametrize("mode", ["int8", "w8a8"])
+@pytest.mark.parametrize("m", [1, 40, 130])
+def test_grouped_qkv_is_one_gemm_over_the_stacked_weight(pkg, dev, mode, m):
+    """The three calls the runner makes (model_runner.py:322-324) on one input: the first runs
+    the stacked (K, Nq + Nk + Nv) GEMM, the other two return their columns of it (no launch of
+    their own: their outputs share its storage), and every module's output equals the stacked
+    product's columns bitwise, with the modules' own buffers still valid packed weights."""
+    from llm_serving_engine_amd.int8_linear import group_qkv
+
+    attn = _attention_projections(pkg, dev, mode)
+    separate = {n: getattr(attn, n) for n in ("q_proj", "k_proj", "v_proj")}
+    unpacked = {n: mod.unpacked_qweight().clone() for n, mod in separate.items()}
+    group = group_qkv(attn)
+    assert group is not None and group.n == 384
+    x = torch.randn(m, 256, device=dev).to(torch.bfloat16)
+    q, k, v = attn.q_proj(x), attn.k_proj(x), attn.v_proj(x)
+    assert q.untyped_storage().data_ptr() == k.untyped_storage().data_ptr() == \
+        v.untyped_storage().data_ptr()
+    stacked = (pkg.ops.w8a16_linear(x, group.qweight, group.scales) if mode == "int8"
+               else pkg.ops.w8a8_linear(x, group.qweight, group.scales))
+    assert torch.equal(torch.cat([q, k, v], -1), stacked)
+    for n, mod in separate.items():
+        assert torch.equal(mod.unpacked_qweight(), unpacked[n])  # views of the stacked weight
+    assert group._out is None, "the product is released once all three took their columns"
+
+
+def test_grouped_qkv_recomputes_for_a_new_or_modified_input(pkg, dev):
+    from llm_serving_engine_amd.int8_linear import group_qkv
+
+    attn = _attention_projections(pkg, dev, "int8")
+    group_qkv(attn)
+    x = torch.randn(5, 256, device=dev).to(torch.bfloat16)
+    q = attn.q_proj(x)
+    x2 = torch.randn(5, 256, device=dev).to(torch.bfloat16)
+    k2 = attn.k_proj(x2)  # another input: computed afresh
+    x.mul_(2.0)  # the first input modified in place: its version moved
+    v = attn.v_proj(x)
+    fresh_k = attn.k_proj(x2)
+    assert torch.equal(k2, fresh_k)
+    q_again, _, v_again = attn.q_proj(x), attn.k_proj(x), attn.v_proj(x)
+    assert torch.equal(v, v_again) and not torch.equal(q, q_again)
+
+
+def test_grouped_qkv_with_bias_and_in_a_graph(pkg, dev):
+    from llm_serving_engine_amd.int8_linear import group_qkv
+
+    attn = _attention_projections(pkg, dev, "int8", bias=True)
+    x = torch.randn(3, 256, device=dev).to(torch.bfloat16)
+    ref = [getattr(attn, n)(x) for n in ("q_proj", "k_proj", "v_proj")]
+    group_qkv(attn)
+    eager = [getattr(attn, n)(x) for n in ("q_proj", "k_proj", "v_proj")]
+    for a, b in zip(ref, eager):  # separate and stacked launches: same tolerance class
+        assert (a.float() - b.float()).abs().max() <= 2e-2 * a.float().abs().max()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [getattr(attn, n)(x) for n in ("q_proj", "k_proj", "v_proj")]
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(eager, outs):
+            assert torch.equal(a, b)
+
+
+def test_quantized_llama_groups_every_layer(pkg, dev):
+    """quantize_model_ groups q/k/v in every layer by default; HF LlamaAttention (three calls on
+    one input, modeling_llama.py:254-256) then gives the logits of the ungrouped model up to the
+    stacked launch's fp32 summation order."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=96, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64,
+                      bos_token_id=None, eos_token_id=None, pad_token_id=None)
+    models = []
+    for fuse_qkv in (True, False):
+        torch.manual_seed(5)
+        with torch.device(dev):
+            models.append(pkg.quantize_model_(
+                LlamaForCausalLM._from_config(cfg, dtype=torch.bfloat16).eval(), "int8",
+                fuse_qkv=fuse_qkv))
+    grouped, plain = models
+    for layer in grouped.model.layers:
+        assert layer.self_attn.k_proj.__dict__.get("_qkv_group") is not None
+    ids = torch.randint(0, 96, (1, 13), device=dev)
+    with torch.no_grad():
+        a, b = grouped(ids).logits.float(), plain(ids).logits.float()
+    assert ((a - b).norm() / b.norm()) < 1e-2
