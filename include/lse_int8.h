@@ -277,7 +277,7 @@ int64_t lse_paged_attention_workspace_bytes(int64_t entries, int64_t H, int64_t 
  * Shapes: D = 128; H a multiple of H_KV with 1 <= H / H_KV <= 16; strides multiples of 8
  *   elements and base pointers 16-byte aligned. max_q_len >= every q_len (a graphed decode may
  *   pass its bucket size). workspace as sized by lse_paged_attention_workspace_bytes.
- * Determinism: each row's keys are summed in fixed 512-position chunks, merged in a fixed order,
+ * Determinism: each row's keys are summed in fixed 1024-position chunks, merged in a fixed order,
  *   so a row's output does not depend on the other entries, the entry count, max_q_len or the
  *   table width (a graph bucket with q_len = 0 padding rows and a pool-wide table gives the bits
  *   an exact-width eager call gives).

@@ -88,12 +88,12 @@ def test_head_groupings(pkg, dev, h, h_kv):
 
 @pytest.mark.parametrize("ctx", [300, 4096, 9000])
 def test_long_contexts_split_into_chunks(pkg, dev, ctx):
-    """Few (entry, head) items over contexts longer than one 512-key chunk take the split path:
+    """Few (entry, head) items over contexts longer than one 1024-key chunk take the split path:
     one workgroup per chunk, folded by a second pass. Deterministic: two calls agree bitwise."""
     c = _case(10 + ctx, [(1, ctx - 1, ctx), (3, ctx - 3, ctx)], block_size=32)
     nbytes = pkg.library().lse_paged_attention_workspace_bytes(
         2, 32, 8, 128, c["max_q_len"], c["table"].shape[1], c["bs"])
-    assert (nbytes > 0) == (ctx > 512), "the split path serves contexts of two chunks or more"
+    assert (nbytes > 0) == (ctx > 1024), "the split path serves contexts of two chunks or more"
     first = _check(pkg, dev, c, f"ctx={ctx}")
     np.testing.assert_array_equal(_run(pkg, dev, c), first)
 
@@ -121,7 +121,7 @@ def test_rows_do_not_depend_on_batch_or_table_width(pkg, dev):
     as the pool, decode_graph.py:97,149) and its eager path (the batch's own entries and table
     width, model_runner.py:268-280) give the same tokens (tests/test_decode_graph.py:53-59). The
     HIP kernel keeps that bitwise: five decode rows over 1 to 2100 keys run as the eager call (40
-    items: one workgroup per 512-key chunk, folded by the second pass), as a 64-entry graph bucket
+    items: one workgroup per 1024-key chunk, folded by the second pass), as a 64-entry graph bucket
     over a pool-wide table (512 items: chunks folded inside one workgroup), with a larger
     max_q_len, and reordered inside another batch."""
     ctxs = [2100, 1, 513, 300, 1030]
@@ -160,12 +160,12 @@ def test_rows_do_not_depend_on_batch_or_table_width(pkg, dev):
 
 
 def test_contexts_beyond_the_split_limit(pkg, dev):
-    """A table spanning more than 64 chunks (32768 keys) runs every item in one workgroup; the
+    """A table spanning more than 64 chunks (65536 keys) runs every item in one workgroup; the
     rows still equal the split launch of a narrower table bitwise."""
     c = _case(70, [(1, 2999, 3000), (2, 998, 1000)], block_size=16)
     base = _run(pkg, dev, c)
     wide = dict(c)
-    width = 2100  # 33600 keys: 66 chunks, no split
+    width = 4200  # 67200 keys: 66 chunks, no split
     lib = pkg.library()
     assert lib.lse_paged_attention_workspace_bytes(2, 32, 8, 128, 2, width, 16) == 0
     assert lib.lse_paged_attention_workspace_bytes(2, 32, 8, 128, 2, c["table"].shape[1], 16) > 0
