@@ -54,6 +54,7 @@ CALIBRATION_BYTES = 64 << 20
 PROFILE_MD = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.md"
 PROFILE_TRAFFIC = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.traffic.json"
 PROFILE_PREFILL = REPO_ROOT / "profiles" / "tiled_gemm_kernel_prefill.md"
+PROFILE_W8A8 = REPO_ROOT / "profiles" / "tiled_gemm_kernel_w8a8.md"
 PROFILE_GLU = REPO_ROOT / "profiles" / "fused_gate_up_kernels.md"
 PROFILE_ATTN = REPO_ROOT / "profiles" / "paged_attn_kernel_decode.md"
 CUS, SIMDS_PER_CU, XCDS = 256, 4, 8
@@ -80,6 +81,8 @@ def parse() -> argparse.Namespace:
                         "--only attention")
     p.add_argument("--summarize-glu", metavar="TRACE",
                    help="write the fused gate_up profile summary from a kernel trace of --only glu")
+    p.add_argument("--summarize-w8a8", nargs=2, metavar=("TRACE", "PMC"),
+                   help="summarize rocprofv3 output dirs of --only w8a8 into profiles/")
     p.add_argument("--summarize-prefill", nargs=2, metavar=("TRACE", "PMC"),
                    help="summarize rocprofv3 output dirs of --only prefill into profiles/")
     return p.parse_args()
@@ -717,6 +720,82 @@ def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
     print("\n".join(out))
 
 
+def summarize_w8a8(trace_dir: str, pmc_dir: str) -> None:
+    """Per (M, shape) duration, TOP/s and int8 MFMA utilisation of the W8A8 tiled GEMM at the
+    prefill-sized M of config 3, from a kernel trace and a counter run of `bench.py --only w8a8`
+    (each M runs one eager pass, then graph replays, each pass the four shapes in order over each
+    rotated weight copy; the decode-range M use other kernels and are left out)."""
+    import csv
+    import statistics
+
+    def read(path):
+        with open(path, newline="") as f:
+            return list(csv.DictReader(f))
+
+    def prefill_gemm(name: str) -> bool:  # the int8 tiled GEMM with the default cache policy
+        head = name.split("(")[0]
+        return "tiled_gemm_kernel<true" in head and head.endswith("false, false>")
+
+    trace = sorted((r for r in read(Path(trace_dir) / "run_kernel_trace.csv")
+                    if prefill_gemm(r["Kernel_Name"])), key=lambda r: int(r["Start_Timestamp"]))
+    pmc_rows = [r for r in read(Path(pmc_dir) / "run_counter_collection.csv")
+                if prefill_gemm(r["Kernel_Name"])]
+    pmc = collections_by_dispatch(pmc_rows, "tiled_gemm_kernel")
+    ms = [m for m in W8A8_MS if m > 64]
+    per_m = len(trace) // len(ms)
+    rows = []
+    for mi, m in enumerate(ms):
+        block = trace[mi * per_m:(mi + 1) * per_m]
+        pblock = pmc[mi * per_m:(mi + 1) * per_m]
+        for si, (k, n) in enumerate(SHAPES):
+            us = statistics.median((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                                   for r in block[si::len(SHAPES)])
+            counters = pblock[si::len(SHAPES)]
+            busy = statistics.median(c["SQ_VALU_MFMA_BUSY_CYCLES"] for c in counters)
+            active = statistics.median(c["GRBM_GUI_ACTIVE"] for c in counters)
+            insts = statistics.median(c["SQ_INSTS_MFMA"] for c in counters)
+            ops = 2.0 * m * n * k
+            name = block[si]["Kernel_Name"].split("(")[0].replace("void lse::", "")
+            cycles = active / XCDS
+            rows.append((m, SHAPE_NAMES[si], k, n, name, us, ops / us / 1e6, insts, busy,
+                         cycles / us / 1e3, busy / (CUS * SIMDS_PER_CU * cycles)))
+    cmds = [
+        "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_w8a8 -o run --output-format csv -- "
+        "python3 bench.py --only w8a8 --steps 8",
+        "rocprofv3 --pmc SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE -d "
+        "gpurun_out/pmc_w8a8 -o run --output-format csv -- python3 bench.py --only w8a8 --steps 8",
+        "python3 bench.py --summarize-w8a8 gpurun_out/prof_w8a8 gpurun_out/pmc_w8a8",
+    ]
+    out = ["# tiled_gemm_kernel<true, ...> — config-3 W8A8 int8 GEMM at prefill M (Llama-3-8B "
+           f"shapes, M in {ms}), one MI355X", "",
+           "Commands (repository root, one MI355X; the last runs on any host):", "", "```", *cmds,
+           "```", "",
+           "frac of 5.0 POP/s: achieved TOP/s (2MNK over the kernel-trace duration of the GEMM "
+           "alone, without the per-token quantizer) over the dense int8 peak. Each "
+           "v_mfma_i32_16x16x64_i8 keeps a SIMD's matrix core busy 16 cycles (SQ_INSTS_MFMA x 16 = "
+           "SQ_VALU_MFMA_BUSY_CYCLES); 256 CUs x 4 SIMDs at 2.4 GHz is the 5.0 POP/s peak. "
+           "GRBM_GUI_ACTIVE, summed over the 8 XCDs, gives the kernel's length in engine clocks "
+           "and so the clock it ran at; MFMA utilisation = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs "
+           "x those clocks). Kernels under ~100 us include launch overhead in the GRBM window "
+           "(implied clocks above 2.4 GHz): read the utilisation of the long ones.", "",
+           "| M | shape (K,N) | kernel | us | TOP/s | frac of 5.0 POP/s | MFMA instrs | MFMA busy "
+           "cycles | clock (GHz) | MFMA utilisation |", "|---|---|---|---|---|---|---|---|---|---|"]
+    for m in ms:
+        tot_o = tot_t = 0.0
+        for rm, sn, k, n, name, us, tops, insts, busy, ghz, util in rows:
+            if rm != m:
+                continue
+            out.append(f"| {m} | {sn} ({k},{n}) | `{name}` | {us:.1f} | {tops:.0f} | "
+                       f"{tops / INT8_PEAK_TOPS:.3f} | {insts:,.0f} | {busy:,.0f} | {ghz:.2f} | "
+                       f"{util:.3f} |")
+            tot_o += 2.0 * m * n * k
+            tot_t += us
+        out.append(f"| {m} | four shapes | | {tot_t:.1f} | {tot_o / tot_t / 1e6:.0f} | "
+                   f"{tot_o / tot_t / 1e6 / INT8_PEAK_TOPS:.3f} | | | | |")
+    PROFILE_W8A8.write_text("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
 def summarize_glu(trace_dir: str) -> None:
     """Per-kernel durations of `bench.py --only glu` from a kernel trace: the fused kernels (last
     template argument true) and the unfused GEMMs and elementwise kernels they replace, grouped
@@ -1007,6 +1086,9 @@ def main() -> None:
         return
     if args.summarize_prefill:
         summarize_prefill(*args.summarize_prefill)
+        return
+    if args.summarize_w8a8:
+        summarize_w8a8(*args.summarize_w8a8)
         return
     if args.summarize_glu:
         summarize_glu(args.summarize_glu)

@@ -613,7 +613,10 @@ static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K, bool glu = fals
   const int mt = M <= 32 ? 2 : 4;
   if (!glu && !nosplit && skinny_split_k(N, K)) return {mt, 4, 4, 4, false, 4};
   const int rt = std::max(skinny_rt(N), glu ? 2 : 1);
-  if (mt == 2) return {2, rt, rt == 4 ? 4 : 8, 4, false, 1};
+  // 17..32 tokens over single-row-tile panels (o_proj, k/v): one wave per SIMD with 4-deep
+  // activation rings keeps more activation bytes in flight than two waves with 2-deep ones; on
+  // MI355X in W8A16 7-10 % faster (o_proj 8.4 against 9.2 us at 32 tokens).
+  if (mt == 2) return {2, rt, rt == 4 || (rt == 1 && !I8) ? 4 : 8, 4, false, 1};
   // 64 tokens: two waves per SIMD (eight per workgroup); a weight ring of 4 for single row
   // tiles (o_proj: 5 % faster than one wave per SIMD), 2 for 32- and 64-row panels.
   return rt == 1 ? SkinnyShape{4, 1, 8, 4, false, 1} : SkinnyShape{4, rt, 8, 2, false, 1};
@@ -629,9 +632,12 @@ static const void* skinny_kernel_for(const SkinnyShape& sh) {
     if (sh.mt == 1)
       return sh.xlds ? skinny_fn<I8, 1, 1, 8, 4, 1, true, false, BFW>()
                      : skinny_fn<I8, 1, 1, 8, 4, 4, false, false, BFW>();
-    if (sh.rt == 1)
-      return sh.mt == 2 ? skinny_fn<I8, 2, 1, 8, 4, 4, false, false, BFW>()
-                        : skinny_fn<I8, 4, 1, 8, 4, 2, false, false, BFW>();
+    if (sh.rt == 1) {
+      if (sh.mt == 2)
+        return sh.w == 4 ? skinny_fn<I8, 2, 1, 4, 4, 4, false, false, BFW>()
+                         : skinny_fn<I8, 2, 1, 8, 4, 4, false, false, BFW>();
+      return skinny_fn<I8, 4, 1, 8, 4, 2, false, false, BFW>();
+    }
     if constexpr (!BFW)
       if (sh.mt == 4 && sh.rt == 4 && sh.w == 4) return skinny_fn<I8, 4, 4, 4, 4, 2, false>();
   }
