@@ -647,10 +647,15 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> None:
     print("\n".join(out))
 
 
-def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
-    """Per (M, shape) duration, TFLOP/s and MFMA utilisation of the tiled kernel from a kernel
-    trace and a counter run of `bench.py --only prefill` (each M runs one eager pass, then graph
-    replays; every pass calls the four shapes in order, over each rotated weight copy)."""
+def tiled_calls(trace_dir: str, pmc_dir: str, keep, ms: list[int], k_per_mfma: int,
+                passes: int) -> list[tuple]:
+    """The tiled GEMM's calls in a kernel trace and a counter run of the same bench command,
+    one row per (M, shape): (m, shape name, k, n, kernel names, median us, MFMA instructions,
+    MFMA busy cycles, engine clocks), each a median over the calls of the sum over the call's
+    dispatches. A call is one dispatch, or two when the GEMM re-tiles the columns of a partial
+    last round; consecutive dispatches are grouped into calls by their MFMA instruction counts,
+    which sum to the call's (M/16)(N/16)(K/k_per_mfma). `keep` selects the kernel names; every
+    M runs `passes` passes over the four shapes in order."""
     import csv
     import statistics
 
@@ -659,30 +664,53 @@ def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
             return list(csv.DictReader(f))
 
     trace = sorted((r for r in read(Path(trace_dir) / "run_kernel_trace.csv")
-                    if "tiled_gemm_kernel" in r["Kernel_Name"]),
-                   key=lambda r: int(r["Start_Timestamp"]))
-    pmc = collections_by_dispatch(read(Path(pmc_dir) / "run_counter_collection.csv"),
-                                  "tiled_gemm_kernel")
-    per_m = len(trace) // len(PREFILL_MS)
+                    if keep(r["Kernel_Name"])), key=lambda r: int(r["Start_Timestamp"]))
+    pmc = collections_by_dispatch([r for r in read(Path(pmc_dir) / "run_counter_collection.csv")
+                                   if keep(r["Kernel_Name"])], "tiled_gemm_kernel")
+    if len(trace) != len(pmc):
+        raise RuntimeError(f"{len(trace)} traced dispatches but {len(pmc)} counted")
+    calls: dict = {}
+    i = 0
+    for m in ms:
+        for _ in range(passes):
+            for si, (k, n) in enumerate(SHAPES):
+                expect = (m // 16) * (n // 16) * (k // k_per_mfma)
+                got, idx = 0, []
+                while got < expect:
+                    got += pmc[i]["SQ_INSTS_MFMA"]
+                    idx.append(i)
+                    i += 1
+                if got != expect:
+                    raise RuntimeError(f"dispatches {idx} of M={m} {SHAPE_NAMES[si]}: {got} MFMA "
+                                       f"instructions, expected {expect}")
+                calls.setdefault((m, si), []).append(idx)
     rows = []
-    for mi, m in enumerate(PREFILL_MS):
-        block = trace[mi * per_m:(mi + 1) * per_m]
-        pblock = pmc[mi * per_m:(mi + 1) * per_m]
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
+    for m in ms:
         for si, (k, n) in enumerate(SHAPES):
-            ds = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-                  for r in block[si::len(SHAPES)]]
-            us = statistics.median(ds)
-            counters = pblock[si::len(SHAPES)]
-            busy = statistics.median(c["SQ_VALU_MFMA_BUSY_CYCLES"] for c in counters)
-            active = statistics.median(c["GRBM_GUI_ACTIVE"] for c in counters)
-            insts = statistics.median(c["SQ_INSTS_MFMA"] for c in counters)
-            flops = 2.0 * m * n * k
-            name = block[si]["Kernel_Name"].split("(")[0].replace("void lse::", "")
-            # GRBM_GUI_ACTIVE comes summed over the XCDs: per XCD it is the kernel's length in
-            # engine clocks, which gives the clock the kernel actually ran at.
-            cycles = active / XCDS
-            rows.append((m, SHAPE_NAMES[si], k, n, name, us, flops / us / 1e6, insts, busy,
-                         cycles / us / 1e3, busy / (CUS * SIMDS_PER_CU * cycles)))
+            cs = calls[(m, si)]
+            med = lambda f: statistics.median(sum(f(j) for j in c) for c in cs)  # noqa: E731
+            names = " + ".join(f"`{trace[j]['Kernel_Name'].split('(')[0].replace('void lse::', '')}`"
+                               for j in cs[0])
+            rows.append((m, SHAPE_NAMES[si], k, n, names, med(lambda j: dur(trace[j])),
+                         med(lambda j: pmc[j]["SQ_INSTS_MFMA"]),
+                         med(lambda j: pmc[j]["SQ_VALU_MFMA_BUSY_CYCLES"]),
+                         med(lambda j: pmc[j]["GRBM_GUI_ACTIVE"]) / XCDS))
+    return rows
+
+
+def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
+    """Per (M, shape) duration, TFLOP/s and MFMA utilisation of the tiled kernel from a kernel
+    trace and a counter run of `bench.py --only prefill` (each M runs one eager pass, then three
+    graph replays, LAYERS passes each; every pass calls the four shapes in order)."""
+    rows = []
+    # GRBM_GUI_ACTIVE comes summed over the XCDs: per XCD it is the kernel's length in engine
+    # clocks, which gives the clock the kernel actually ran at.
+    for m, sn, k, n, name, us, insts, busy, cycles in tiled_calls(
+            trace_dir, pmc_dir, lambda name: "tiled_gemm_kernel" in name, PREFILL_MS, 32,
+            4 * LAYERS):
+        rows.append((m, sn, k, n, name, us, 2.0 * m * n * k / us / 1e6, insts, busy,
+                     cycles / us / 1e3, busy / (CUS * SIMDS_PER_CU * cycles)))
     cmds = [
         "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_prefill -o run --output-format csv "
         "-- python3 bench.py --only prefill --steps 8",
@@ -709,7 +737,7 @@ def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
            "cycles | clock (GHz) | MFMA utilisation |", "|---|---|---|---|---|---|---|---|---|---|"]
     tot_f = tot_t = 0.0
     for m, sn, k, n, name, us, tf, insts, busy, ghz, util in rows:
-        out.append(f"| {m} | {sn} ({k},{n}) | `{name}` | {us:.1f} | {tf:.0f} | {tf / 2500:.3f} | "
+        out.append(f"| {m} | {sn} ({k},{n}) | {name} | {us:.1f} | {tf:.0f} | {tf / 2500:.3f} | "
                    f"{insts:,.0f} | {busy:,.0f} | {ghz:.2f} | {util:.3f} |")
         if m == 2048:
             tot_f += 2.0 * m * n * k
@@ -723,42 +751,19 @@ def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
 def summarize_w8a8(trace_dir: str, pmc_dir: str) -> None:
     """Per (M, shape) duration, TOP/s and int8 MFMA utilisation of the W8A8 tiled GEMM at the
     prefill-sized M of config 3, from a kernel trace and a counter run of `bench.py --only w8a8`
-    (each M runs one eager pass, then graph replays, each pass the four shapes in order over each
-    rotated weight copy; the decode-range M use other kernels and are left out)."""
-    import csv
-    import statistics
-
-    def read(path):
-        with open(path, newline="") as f:
-            return list(csv.DictReader(f))
-
+    (each M runs one eager pass, then three graph replays at `--steps 8`, LAYERS passes each,
+    every pass the four shapes in order; the decode-range M use other kernels and are left
+    out)."""
     def prefill_gemm(name: str) -> bool:  # the int8 tiled GEMM with the default cache policy
         head = name.split("(")[0]
         return "tiled_gemm_kernel<true" in head and head.endswith("false, false>")
 
-    trace = sorted((r for r in read(Path(trace_dir) / "run_kernel_trace.csv")
-                    if prefill_gemm(r["Kernel_Name"])), key=lambda r: int(r["Start_Timestamp"]))
-    pmc_rows = [r for r in read(Path(pmc_dir) / "run_counter_collection.csv")
-                if prefill_gemm(r["Kernel_Name"])]
-    pmc = collections_by_dispatch(pmc_rows, "tiled_gemm_kernel")
     ms = [m for m in W8A8_MS if m > 64]
-    per_m = len(trace) // len(ms)
     rows = []
-    for mi, m in enumerate(ms):
-        block = trace[mi * per_m:(mi + 1) * per_m]
-        pblock = pmc[mi * per_m:(mi + 1) * per_m]
-        for si, (k, n) in enumerate(SHAPES):
-            us = statistics.median((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-                                   for r in block[si::len(SHAPES)])
-            counters = pblock[si::len(SHAPES)]
-            busy = statistics.median(c["SQ_VALU_MFMA_BUSY_CYCLES"] for c in counters)
-            active = statistics.median(c["GRBM_GUI_ACTIVE"] for c in counters)
-            insts = statistics.median(c["SQ_INSTS_MFMA"] for c in counters)
-            ops = 2.0 * m * n * k
-            name = block[si]["Kernel_Name"].split("(")[0].replace("void lse::", "")
-            cycles = active / XCDS
-            rows.append((m, SHAPE_NAMES[si], k, n, name, us, ops / us / 1e6, insts, busy,
-                         cycles / us / 1e3, busy / (CUS * SIMDS_PER_CU * cycles)))
+    for m, sn, k, n, name, us, insts, busy, cycles in tiled_calls(
+            trace_dir, pmc_dir, prefill_gemm, ms, 64, 4 * LAYERS):
+        rows.append((m, sn, k, n, name, us, 2.0 * m * n * k / us / 1e6, insts, busy,
+                     cycles / us / 1e3, busy / (CUS * SIMDS_PER_CU * cycles)))
     cmds = [
         "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_w8a8 -o run --output-format csv -- "
         "python3 bench.py --only w8a8 --steps 8",
@@ -785,7 +790,7 @@ def summarize_w8a8(trace_dir: str, pmc_dir: str) -> None:
         for rm, sn, k, n, name, us, tops, insts, busy, ghz, util in rows:
             if rm != m:
                 continue
-            out.append(f"| {m} | {sn} ({k},{n}) | `{name}` | {us:.1f} | {tops:.0f} | "
+            out.append(f"| {m} | {sn} ({k},{n}) | {name} | {us:.1f} | {tops:.0f} | "
                        f"{tops / INT8_PEAK_TOPS:.3f} | {insts:,.0f} | {busy:,.0f} | {ghz:.2f} | "
                        f"{util:.3f} |")
             tot_o += 2.0 * m * n * k

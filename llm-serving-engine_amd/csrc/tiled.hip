@@ -61,6 +61,7 @@ struct TiledArgs {
   int nrb;           // ceil(N / 16)
   int mblocks, nblocks;
   int glu;           // gate/up layout: I, the output columns (N = 16 nrb packed rows); else 0
+  int glu_up;        //   and the offset of the up scales from the gate scales in s
   int splits;        // > 1 (no gate/up): K split into ranges of ssteps steps, raw partial sums
   int ssteps;        //   (fp32, or int32 in W8A8) to part, added by the decode kernel's second
   void* part;        //   pass; [splits][M][16 nrb]
@@ -352,7 +353,7 @@ tiled_gemm_kernel(TiledArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           sg[r] = r < cnt ? a.s[n + r] : 0.0f;
-          su[r] = r < cnt ? a.s[a.glu + n + r] : 0.0f;
+          su[r] = r < cnt ? a.s[a.glu_up + n + r] : 0.0f;
         }
         store_glu4<I8>(a.y, a.ldy, m, n, cnt, acc[i][j], acc[i][j + 1], sg, su, sxm, yvec);
       }
@@ -445,7 +446,7 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false) {
 // the Llama-3-8B prefill shapes timed (qkv, o_proj, gate_up, down at M = 256 to 2048, gate_up at
 // 8192) this picks the fastest tile, or one within 6 % (qkv at M = 512).
 template <bool I8>
-static TiledShape tiled_shape(int64_t M, int64_t N, int cus) {
+static TiledShape tiled_shape(int64_t M, int64_t N, int cus, double* cost_out = nullptr) {
   // The 64 x 128 tile (four waves) fills the CUs when M is a few hundred and N is narrow, e.g.
   // o_proj and down at M = 256..512: 16-25 % faster than 128 x 128 there, in both modes.
   static const TiledShape cand[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 128}};
@@ -462,6 +463,7 @@ static TiledShape tiled_shape(int64_t M, int64_t N, int cus) {
       best = cand[i];
     }
   }
+  if (cost_out) *cost_out = best_cost;
   return best;
 }
 
@@ -475,7 +477,49 @@ static int device_cus() {
   return cus;
 }
 
+// One launch of tile shape `sh` over packed weight rows [n0, n0 + n) (a multiple of 32 rows in
+// the gate/up layout, so it starts at a gate/up pair): the operands are offset to that range.
 // glu > 0: the gate/up layout of two (glu, K) matrices, N = 2 x 16 ceil(glu / 16) packed rows.
+template <bool I8>
+static int launch_tiled_range(const TiledShape& sh, bool decode, const void* x, int64_t ldx,
+                              const int8_t* qp, const float* s, const float* sx, uint16_t* y,
+                              int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
+                              int64_t glu, int64_t n0, int64_t n, hipStream_t stream) {
+  const int threads = sh.bm <= 64 ? 256 : kTiledThreads;
+  TiledArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.qp = qp + (n0 / kTileRows) * ceil_div(K, kTileK) * kTileBytes;
+  a.s = s + (glu > 0 ? n0 / 2 : n0);
+  a.sx = sx;
+  a.y = y ? y + (glu > 0 ? n0 / 2 : n0) : nullptr;
+  a.ldy = ldy;
+  a.acc = acc;  // whole-range launches only (acc rows are N long)
+  a.M = (int)M;
+  a.N = (int)n;
+  a.K = (int)K;
+  a.nsteps = (int)ceil_div(K, kTileK);
+  a.nrb = (int)ceil_div(n, kTileRows);
+  a.mblocks = (int)ceil_div(M, sh.bm);
+  a.nblocks = (int)ceil_div(n, sh.bn);
+  a.glu = glu > 0 ? (int)(glu - n0 / 2) : 0;
+  a.glu_up = (int)glu;
+  const int64_t blocks = (int64_t)a.mblocks * a.nblocks;
+  if (blocks > 0x7fffffff) return LSE_E_RANGE;
+  void* args[] = {&a};
+  const void* fn = glu > 0 ? tiled_kernel_for<I8, true>(sh, decode)
+                            : tiled_kernel_for<I8, false>(sh, decode);
+  const hipError_t e =
+      hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(threads), args, 0, stream);
+  return e == hipSuccess ? launch_status() : (int)e;
+}
+
+// The cost model's tile over all N, except when its tiles leave a partial last round on the CUs
+// (gate_up at M = 2048: 896 tiles of 256 x 256 for 256 CUs, 3.5 rounds) and re-tiling the
+// columns of that round fills them better: then the full rounds run as one launch and the
+// remaining columns, with the cost model's tile for them, as a second (gate_up at M = 2048: 768
+// tiles of 256 x 256, then 256 of 128 x 256 over the last 4096 rows). Every output sums its K
+// steps in increasing order whatever the tile, so the split changes no result.
 // `wide_decode`: the 32 x 128 or 64 x 128 tile of launch_w8a16_wide_decode instead of the cost
 // model's.
 template <bool I8>
@@ -484,34 +528,34 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
                         int64_t N, int64_t K, int64_t glu, hipStream_t stream,
                         bool wide_decode = false) {
   if (glu > 0) N = 2 * kTileRows * ceil_div(glu, kTileRows);
-  const TiledShape sh = wide_decode ? TiledShape{(I8 || M > 32) ? 64 : 32, 128}
-                                    : tiled_shape<I8>(M, N, device_cus());
-  const int threads = sh.bm <= 64 ? 256 : kTiledThreads;
-  TiledArgs a{};
-  a.x = x;
-  a.ldx = ldx;
-  a.qp = qp;
-  a.s = s;
-  a.sx = sx;
-  a.y = y;
-  a.ldy = ldy;
-  a.acc = acc;
-  a.M = (int)M;
-  a.N = (int)N;
-  a.K = (int)K;
-  a.nsteps = (int)ceil_div(K, kTileK);
-  a.nrb = (int)ceil_div(N, kTileRows);
-  a.mblocks = (int)ceil_div(M, sh.bm);
-  a.nblocks = (int)ceil_div(N, sh.bn);
-  a.glu = (int)glu;
-  const int64_t blocks = (int64_t)a.mblocks * a.nblocks;
-  if (blocks > 0x7fffffff) return LSE_E_RANGE;
-  void* args[] = {&a};
-  const void* fn = glu > 0 ? tiled_kernel_for<I8, true>(sh, wide_decode)
-                            : tiled_kernel_for<I8, false>(sh, wide_decode);
-  const hipError_t e =
-      hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(threads), args, 0, stream);
-  return e == hipSuccess ? launch_status() : (int)e;
+  if (wide_decode) {
+    const TiledShape sh{(I8 || M > 32) ? 64 : 32, 128};
+    return launch_tiled_range<I8>(sh, true, x, ldx, qp, s, sx, y, ldy, acc, M, N, K, glu, 0, N,
+                                  stream);
+  }
+  const int cus = device_cus();
+  double cost = 0.0;
+  const TiledShape sh = tiled_shape<I8>(M, N, cus, &cost);
+  const int64_t mblocks = ceil_div(M, sh.bm);
+  const int64_t blocks = mblocks * ceil_div(N, sh.bn);
+  const int64_t full = blocks / cus;  // whole rounds of the chosen tile
+  if (!acc && full >= 1 && blocks % cus && (full * cus) % mblocks == 0) {
+    const int64_t n_bulk = full * cus / mblocks * sh.bn;
+    if (n_bulk < N) {
+      double tail_cost = 0.0;
+      const TiledShape tsh = tiled_shape<I8>(M, N - n_bulk, cus, &tail_cost);
+      const double bulk_cost = cost * full / (full + 1);  // `full` of the full + 1 rounds
+      if (bulk_cost + tail_cost < 0.97 * cost) {
+        if (int st = launch_tiled_range<I8>(sh, false, x, ldx, qp, s, sx, y, ldy, nullptr, M, N,
+                                            K, glu, 0, n_bulk, stream))
+          return st;
+        return launch_tiled_range<I8>(tsh, false, x, ldx, qp, s, sx, y, ldy, nullptr, M, N, K,
+                                      glu, n_bulk, N - n_bulk, stream);
+      }
+    }
+  }
+  return launch_tiled_range<I8>(sh, false, x, ldx, qp, s, sx, y, ldy, acc, M, N, K, glu, 0, N,
+                                stream);
 }
 
 int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
