@@ -425,17 +425,18 @@ def bench_glu(pkg, dev, steps: int, gen) -> dict:
 
 
 def bench_lm_head(pkg, dev, steps: int, gen) -> dict:
-    """The bf16 lm_head of Llama-3 (N = 128256, K = 4096, 1.05 GB) at decode batch sizes: the
-    decode kernel on the bf16 tile layout against torch's F.linear (the vendor BLAS, the
-    reference's own call), us and GB/s (2NK + 2MK + 2MN bytes), over 2 weight copies so every
-    call streams its weight from HBM."""
+    """The bf16 lm_head of Llama-3 (N = 128256, K = 4096, 1.05 GB) at decode batch sizes and at
+    the row counts a prefill step's `emit_owed` passes (one row per sequence): the packed bf16
+    path (`lse_bf16_decode_gemm`) against torch's F.linear (the vendor BLAS, the reference's own
+    call), us and GB/s (2NK + 2MK + 2MN bytes), over 2 weight copies so every call streams its
+    weight from HBM."""
     import torch
 
     n, k = 128256, 4096
     ws = [(torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(dev) for _ in range(2)]
     wps = [pkg.ops.pack_bf16_weight(w) for w in ws]
     res = {}
-    for m in DECODE_MS:
+    for m in DECODE_MS + [128, 256]:
         x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
         ours = lambda x=x: [pkg.ops.bf16_decode_linear(x, wp, n) for wp in wps]  # noqa: E731
         blas = lambda x=x: [torch.nn.functional.linear(x, w) for w in ws]  # noqa: E731
@@ -1055,6 +1056,7 @@ def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
     note("whole steps timed")
     h = torch.randn(batch, model.config.hidden_size, generator=gen).to(torch.bfloat16).to(dev)
     t_head = time_graph(lambda: model.lm_head(h), steps)
+    t_head_packed = time_graph(lambda: runner.head(h), steps)
     head_bytes = 2 * model.lm_head.weight.numel()
     margin = torch.cat(margins)
     return {
@@ -1072,6 +1074,8 @@ def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
             float((paged_logits - torch_logits).norm() / torch_logits.norm()), 5),
         "lm_head_bf16_us": round(t_head * 1e6, 1),
         "lm_head_gbps": round(head_bytes / t_head / 1e9, 1),
+        "lm_head_packed_us": round(t_head_packed * 1e6, 1),
+        "lm_head_packed_gbps": round(head_bytes / t_head_packed / 1e9, 1),
         "greedy_match_rate": round(match / (batch * decode_steps), 4),
         "greedy_match_rate_vs_int8_torch_restatement": round(
             match_torch / (batch * decode_steps), 4),

@@ -79,7 +79,7 @@ enum lse_query_key {
   LSE_Q_NOALLOC_SCRATCH = 5, /* bytes of the static scratch lse_w8a16_gemm_noalloc works in */
 };
 
-#define LSE_ABI_VERSION 9
+#define LSE_ABI_VERSION 10
 #define LSE_NOALLOC_SCRATCH_BYTES (16 << 20)
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
@@ -311,11 +311,12 @@ int lse_pack_bf16_weight(const void* w, int64_t ldw, int64_t N, int64_t K, void*
                          void* stream);
 
 /*
- * bf16 linear for decode-sized batches (the lm_head the int8 path keeps in bf16):
- *   y[m,n] = bf16_rne(sum_k x[m,k] * w[n,k]), fp32 accumulation, M <= LSE_DECODE_MAX_M.
+ * bf16 linear over the packed bf16 layout (the lm_head the int8 path keeps in bf16), built for
+ * decode-sized batches and correct for any M:
+ *   y[m,n] = bf16_rne(sum_k x[m,k] * w[n,k]), fp32 accumulation.
  * x: (M, K) bf16, row stride ldx (multiple of 8, 16-byte aligned). wp: lse_pack_bf16_weight
- * layout. y: (M, N) bf16, row stride ldy >= N. Deterministic as the int8 decode GEMMs are.
- * Returns LSE_E_ALGO for M > LSE_DECODE_MAX_M.
+ * layout. y: (M, N) bf16, row stride ldy >= N. Deterministic as the int8 decode GEMMs are: a
+ * row's bits depend on N, K and its token class (1..16, 17..32, 33..64, above 64) only.
  * Replaces: `F.linear(hidden, lm_head.weight)` in `emit_owed` (model_runner.py:306-307) and the
  * graphed decode step (decode_graph.py:140).
  */

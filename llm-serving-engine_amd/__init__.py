@@ -13,6 +13,7 @@ from .int8_linear import (
     Int8GluMLP,
     Int8Linear,
     Int8RMSNormQuant,
+    PackedBf16Linear,
     QuantizedRows,
     check_linear_supported,
 )
@@ -25,6 +26,7 @@ __all__ = [
     "Int8Linear",
     "Int8RMSNormQuant",
     "ModelConfig",
+    "PackedBf16Linear",
     "QuantizedRows",
     "check_int8_support",
     "check_linear_supported",

@@ -29,7 +29,8 @@ import torch
 from torch import nn
 
 from . import ops
-from .int8_linear import Int8GateUp, Int8GluMLP, Int8Linear, Int8RMSNormQuant, group_qkv
+from .int8_linear import (Int8GateUp, Int8GluMLP, Int8Linear, Int8RMSNormQuant, PackedBf16Linear,
+                          group_qkv)
 
 FORMAT = "lse-int8"
 MODEL_TYPES = ("llama",)  # architectures the loader rebuilds (LlamaForCausalLM)
@@ -96,13 +97,19 @@ def save_int8_checkpoint(model: nn.Module, path: str | Path) -> Path:
 
     _check_model_type(getattr(model.config, "model_type", None))
     tensors, mode = _quantized_tensors(model)
-    for name, t in model.state_dict().items():
+    tied = getattr(model.config, "tie_word_embeddings", False)
+    state = model.state_dict()
+    head = getattr(model, "lm_head", None)
+    if isinstance(head, PackedBf16Linear):  # stored row-major, as an unquantized lm_head is
+        state.pop("lm_head.wp")
+        if not tied:
+            state["lm_head.weight"] = head.unpacked_weight()
+    for name, t in state.items():
         if t.is_floating_point() and not name.endswith((".qweight", ".scales")):
             owner = name.rsplit(".", 1)[0]
             if any(owner.endswith(f".{p}") for p in ATTENTION + MLP) or ".gate_up." in name:
                 continue
-            if name.endswith("lm_head.weight") and getattr(model.config, "tie_word_embeddings",
-                                                           False):
+            if name.endswith("lm_head.weight") and tied:
                 continue  # tied to embed_tokens.weight
             tensors[name] = t.detach().to(torch.bfloat16).cpu().contiguous()
     meta = {"format": FORMAT, "format_version": FORMAT_VERSION, "mode": mode,
@@ -137,10 +144,12 @@ def _materialize_meta(model: nn.Module, device: torch.device) -> None:
 
 
 @torch.no_grad()
-def load_int8_checkpoint(path: str | Path, device: torch.device | str = "cuda") -> nn.Module:
+def load_int8_checkpoint(path: str | Path, device: torch.device | str = "cuda",
+                         pack_lm_head: bool = True) -> nn.Module:
     """A `LlamaForCausalLM` with int8 projections from a checkpoint written by
     `save_int8_checkpoint`. bf16 projection weights are never allocated: the skeleton is built
-    on the meta device and the int8 buffers are filled (and packed) on `device`."""
+    on the meta device and the int8 buffers are filled (and packed) on `device`. With
+    `pack_lm_head` the lm_head becomes `PackedBf16Linear`, as `quantize_model_` leaves it."""
     from safetensors import safe_open
     from transformers import AutoConfig, LlamaForCausalLM
 
@@ -199,5 +208,7 @@ def load_int8_checkpoint(path: str | Path, device: torch.device | str = "cuda") 
         for layer in model.model.layers:
             for name in ("input_layernorm", "post_attention_layernorm"):
                 setattr(layer, name, Int8RMSNormQuant(getattr(layer, name)))
+    if pack_lm_head and isinstance(model.lm_head, nn.Linear) and model.lm_head.bias is None:
+        model.lm_head = PackedBf16Linear.from_linear(model.lm_head)
     ops._require(all(not p.is_meta for p in model.parameters()), "parameters left on meta")
     return model

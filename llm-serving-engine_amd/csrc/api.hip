@@ -444,7 +444,6 @@ int lse_bf16_decode_gemm(const void* x, int64_t ldx, const void* wp, void* y, in
                          int64_t M, int64_t N, int64_t K, void* stream) {
   if (M < 0 || N < 0 || K < 0 || N > kMaxRows) return LSE_E_SHAPE;
   if (K % LSE_K_ALIGN) return LSE_E_ALIGN;
-  if (M > LSE_DECODE_MAX_M) return LSE_E_ALGO;
   if (M == 0 || N == 0) return LSE_OK;
   if (!wp) return LSE_E_NULL;
   if (!aligned(wp, 16)) return LSE_E_ALIGN;

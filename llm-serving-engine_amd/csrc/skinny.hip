@@ -874,8 +874,16 @@ int launch_w8a8_skinny_glu(const int8_t* xq, const float* sx, const int8_t* qp, 
 
 namespace lse {
 
+int launch_bf16_tiled(const uint16_t* x, int64_t ldx, const uint16_t* wp, uint16_t* y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream);  // tiled.hip
+
+// bf16 weights: this kernel up to 16 tokens (and up to 64 over narrow weights), the tiled
+// kernel's bf16 tiles where this kernel's gate_up-class rule sends int8 weights to tiles
+// (17..64 tokens over at least 1024 row tiles, the lm_head) and beyond 64 tokens.
 int launch_bf16_skinny(const uint16_t* x, int64_t ldx, const uint16_t* wp, uint16_t* y,
                        int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  if (M > LSE_DECODE_MAX_M || skinny_wide_tiled(M, N))
+    return launch_bf16_tiled(x, ldx, wp, y, ldy, M, N, K, stream);
   return skinny_run<false>(x, ldx, reinterpret_cast<const int8_t*>(wp), nullptr, nullptr, y, ldy,
                            nullptr, M, N, K, 0, nullptr, 0, stream, true);
 }

@@ -26,7 +26,9 @@ applies o_proj (`attention_output`, model_runner.py:365-369).
 With `trace` set to a list, every int8 projection of a step appends (layer, name, input,
 output), so each layer's kernels can be checked on the very input they saw (errors do not
 compound over layers).
-lm_head stays bf16 in both. Attention has two implementations: "torch", fp32 over a
+lm_head stays bf16 in every back end: the vendor BLAS's `nn.Linear` on "bf16" and "int8-torch",
+`PackedBf16Linear` (the same bf16 weight in the packed tile layout, `quantize_model_`'s default)
+on "int8", in either quantization mode. Attention has two implementations: "torch", fp32 over a
 contiguous per-layer KV cache (the reference's `contiguous_attention` path,
 model_runner.py:400-418), the same arithmetic for both linear back ends so only the linears
 differ; and "paged", the HIP paged attention (`ops.paged_attention_forward`, the reference's
@@ -43,7 +45,7 @@ import torch
 from torch import nn
 
 from . import ops
-from .int8_linear import Int8GateUp, Int8Linear
+from .int8_linear import Int8GateUp, Int8Linear, PackedBf16Linear
 
 LLAMA3_8B = dict(
     hidden_size=4096,
@@ -90,6 +92,7 @@ class DecodeRunner:
         self.k_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
         self.v_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in self.layers]
         self.int8: list[dict[str, Int8Linear]] | None = None
+        self.head: PackedBf16Linear | None = None
         self.trace: list | None = None
         self.backend = "bf16"
         self.attention = "torch"
@@ -158,6 +161,8 @@ class DecodeRunner:
                 "down": _int8(mlp.down_proj.weight, mode),
             })
             del qkv
+        head = self.model.lm_head
+        self.head = head if isinstance(head, PackedBf16Linear) else PackedBf16Linear.from_linear(head)
         torch.cuda.empty_cache()
 
     def use(self, backend: str) -> None:
@@ -261,7 +266,11 @@ class DecodeRunner:
         """One decode step: tokens (batch,) at `position` -> bf16 logits (batch, vocab) from the
         bf16 lm_head (the reference's emit_owed)."""
         hidden = self.forward(tokens[:, None], position)
-        return self.model.lm_head(hidden[0])
+        return self.lm_head()(hidden[0])
+
+    def lm_head(self) -> nn.Module:
+        """The back end's lm_head: the packed bf16 one on "int8", the model's own otherwise."""
+        return self.head if self.backend == "int8" and self.head is not None else self.model.lm_head
 
     # ---- linear-only timing -------------------------------------------------------------------
 

@@ -351,3 +351,51 @@ class Int8RMSNormQuant(nn.Module):
 
     def extra_repr(self) -> str:
         return f"{tuple(self.weight.shape)}, eps={self.variance_epsilon}, quantize=per-token int8"
+
+
+class PackedBf16Linear(nn.Module):
+    """Drop-in for the bf16 `lm_head` (`nn.Linear(K, N, bias=False)`) the int8 path keeps in
+    bf16: the reference calls it as `get_output_embeddings()(hidden)` (model_runner.py:306-307,
+    decode_graph.py:140), which this module's `forward(x) -> y` serves. The weight is held in the
+    packed bf16 tile layout (`ops.pack_bf16_weight`, buffer `wp`, the same bytes as the bf16
+    matrix) and the product runs as `lse_bf16_decode_gemm`: the decode kernel up to 16 rows and
+    bf16 tiles of the tiled kernel above. `unpacked_weight()` returns the row-major matrix."""
+
+    def __init__(self, in_features: int, out_features: int,
+                 device: torch.device | str | None = None) -> None:
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.register_buffer(
+            "wp",
+            torch.zeros(ops.packed_bf16_shape(out_features, in_features), dtype=torch.bfloat16,
+                        device=device),
+        )
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear) -> PackedBf16Linear:
+        """Packs `linear.weight` (bf16, on the GPU, no bias) on its own device."""
+        w = linear.weight.detach()
+        if linear.bias is not None:
+            raise RuntimeError("the packed bf16 linear has no bias term")
+        if w.dtype != torch.bfloat16:
+            raise RuntimeError(f"the packed bf16 linear needs a bf16 weight, got {w.dtype}")
+        if w.device.type != "cuda":
+            raise RuntimeError(f"the packed bf16 linear needs a CUDA (HIP) device, got {w.device}")
+        k_align = _lib.query(_lib.Q_K_ALIGN)
+        if linear.in_features % k_align:
+            raise RuntimeError(f"the packed bf16 linear needs in_features % {k_align} == 0, got "
+                               f"{linear.in_features}")
+        mod = cls(linear.in_features, linear.out_features, w.device)
+        mod.wp.copy_(ops.pack_bf16_weight(w))
+        return mod
+
+    def unpacked_weight(self) -> torch.Tensor:
+        """The bf16 weight as a row-major (N, K) matrix."""
+        return ops.unpack_bf16_weight(self.wp, self.out_features, self.in_features)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return ops.bf16_decode_linear(x, self.wp, self.out_features)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, packed bf16"

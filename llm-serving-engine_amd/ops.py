@@ -20,6 +20,7 @@ __all__ = [
     "bf16_decode_linear",
     "pack_bf16_weight",
     "packed_bf16_shape",
+    "unpack_bf16_weight",
     "paged_attention_forward",
     "pack_glu",
     "pack_weight",
@@ -463,9 +464,18 @@ def pack_bf16_weight(w: torch.Tensor) -> torch.Tensor:
     return wp
 
 
+def unpack_bf16_weight(wp: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """Inverse of `pack_bf16_weight` (a pure permutation, done with torch views): (N, K) bf16."""
+    rb, steps, _ = wp.shape
+    t = wp.reshape(rb, steps, 2, 4, 16, 8)  # [rb][step][half][g = lane // 16][row][8 elements]
+    t = t.permute(0, 4, 1, 3, 2, 5).reshape(rb * 16, steps * 64)
+    return t[:n, :k].contiguous()
+
+
 def bf16_decode_linear(x: torch.Tensor, wp: torch.Tensor, n: int) -> torch.Tensor:
-    """y = bf16(x · wᵀ) for x (..., K) bf16 with at most 64 rows, w given packed
-    (`pack_bf16_weight`) → y (..., N) bf16; fp32 accumulation."""
+    """y = bf16(x · wᵀ) for x (..., K) bf16, w given packed (`pack_bf16_weight`) → y (..., N)
+    bf16; fp32 accumulation. Built for decode batches (the decode kernel up to 16 rows, bf16
+    tiles of the tiled kernel above), correct for any number of rows."""
     dev = _on_gpu(x, wp)
     _require(x.dtype == torch.bfloat16, f"expects bf16 activations, got {x.dtype}")
     k = x.shape[-1]

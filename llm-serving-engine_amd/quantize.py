@@ -6,7 +6,8 @@ This is the work the reference's int8 switch stands in for: `ModelRunner.__init_
 `ModelRunner.__init__`, after `from_pretrained(...).to(device)` (model_runner.py:50-52) and
 before any CUDA graph is captured (engine.py:94-106), because a graph freezes kernels and
 tensor addresses. lm_head stays bf16, as the reference's `emit_owed` computes it
-(model_runner.py:306-307).
+(model_runner.py:306-307), but moves to the packed bf16 tile layout (`PackedBf16Linear`), whose
+kernels stream it faster than the vendor BLAS at decode batch sizes.
 """
 
 from __future__ import annotations
@@ -16,8 +17,8 @@ import gc
 import torch
 from torch import nn
 
-from .int8_linear import (MODES, Int8GluMLP, Int8Linear, Int8RMSNormQuant, fusable_mlp,
-                          group_qkv)
+from .int8_linear import (MODES, Int8GluMLP, Int8Linear, Int8RMSNormQuant, PackedBf16Linear,
+                          fusable_mlp, group_qkv)
 
 ATTENTION_PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj")
 MLP_PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
@@ -40,15 +41,17 @@ def check_int8_support(model: nn.Module) -> None:
 
 @torch.no_grad()
 def quantize_model_(model: nn.Module, mode: str = "int8", fuse_mlp: bool = True,
-                    fuse_norm: bool | None = None, fuse_qkv: bool = True) -> nn.Module:
+                    fuse_norm: bool | None = None, fuse_qkv: bool = True,
+                    pack_lm_head: bool = True) -> nn.Module:
     """Replaces q/k/v/o of every decoder layer by `Int8Linear` (per-channel int8 weights
     quantized on the GPU) and its MLP by `Int8GluMLP` (fused gate/up + SiLU-mul, then down), or,
     with `fuse_mlp=False` or an MLP of another form, gate/up/down by `Int8Linear` each. With
     `fuse_qkv` the layer's q, k and v projections share one stacked weight (`QKVGroup`): the
     three module calls the runner makes on one input run as one GEMM. In the W8A8 mode
     (`fuse_norm`, default on for "w8a8") the layer's two RMSNorms become `Int8RMSNormQuant`,
-    which quantizes the normed rows once for all their projections. Returns the same model
-    object."""
+    which quantizes the normed rows once for all their projections. With `pack_lm_head` a bf16
+    `lm_head` without bias becomes `PackedBf16Linear` (same bf16 values, tile layout; a tied
+    lm_head keeps its embedding and adds the packed copy). Returns the same model object."""
     if mode not in MODES:
         raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
     if fuse_norm is None:
@@ -75,6 +78,11 @@ def quantize_model_(model: nn.Module, mode: str = "int8", fuse_mlp: bool = True,
                 norm = getattr(layer, name)
                 if not isinstance(norm, Int8RMSNormQuant):
                     setattr(layer, name, Int8RMSNormQuant(norm))
+    head = getattr(model, "lm_head", None)
+    if (pack_lm_head and isinstance(head, nn.Linear) and head.bias is None
+            and head.weight.dtype == torch.bfloat16):
+        model.lm_head = PackedBf16Linear.from_linear(head)
+        del head
     gc.collect()
     torch.cuda.empty_cache()
     return model

@@ -39,7 +39,22 @@ def test_matches_the_oracle(pkg, dev, m, n, k):
     assert ok, f"M={m} N={n} K={k}: {msg}"
 
 
-@pytest.mark.parametrize("m", [1, 64])
+@pytest.mark.parametrize("m", [17, 32, 33, 64, 65, 200])
+def test_tiles_match_the_oracle(pkg, dev, m):
+    """17..64 tokens over at least 1024 row tiles (the lm_head's class) and every M above 64 run
+    as bf16 tiles of the tiled kernel; N = 16400 is 1025 row tiles, and 16400 % 128 leaves a
+    partial last column tile."""
+    n, k = 16400, 1040
+    rng = np.random.default_rng(m)
+    x = ora.f32_to_bf16_bits(rng.standard_normal((m, k), dtype=np.float32))
+    w = ora.f32_to_bf16_bits(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    wp = pkg.ops.pack_bf16_weight(to_bf16_tensor(w, dev))
+    y = bf16_bits(pkg.ops.bf16_decode_linear(to_bf16_tensor(x, dev), wp, n))
+    ok, msg = ora.within_tolerance(y, ora.bf16_linear_golden(x, w))
+    assert ok, f"M={m}: {msg}"
+
+
+@pytest.mark.parametrize("m", [1, 32, 64])
 def test_llama3_lm_head_shape(pkg, dev, m):
     """N = 128256, K = 4096 against the fp32 product on the GPU and torch's bf16 F.linear."""
     g = torch.Generator(device="cpu").manual_seed(m)
@@ -53,19 +68,17 @@ def test_llama3_lm_head_shape(pkg, dev, m):
     assert (y.float() - blas.float()).abs().max().item() <= 1e-2 * ref.__abs__().max()
 
 
-def test_more_than_64_rows_are_refused(pkg, dev):
-    wp = pkg.ops.pack_bf16_weight(torch.zeros(16, 64, dtype=torch.bfloat16, device=dev))
-    with pytest.raises(RuntimeError, match="algorithm"):
-        pkg.ops.bf16_decode_linear(torch.zeros(65, 64, dtype=torch.bfloat16, device=dev), wp, 16)
-
-
-def test_batch_invariant_and_deterministic(pkg, dev):
+@pytest.mark.parametrize("n", [3000, 16400])
+def test_batch_invariant_and_deterministic(pkg, dev, n):
+    """Inside each token class a row's bits do not depend on M: the decode kernel's classes over
+    a narrow weight (3000 rows), the bf16 tiles' over a wide one (16400 rows, 1025 row tiles),
+    and beyond 64 tokens."""
     g = torch.Generator(device="cpu").manual_seed(9)
-    w = (torch.randn(3000, 2048, generator=g) * 0.02).to(torch.bfloat16).to(dev)
-    x = torch.randn(64, 2048, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(n, 2048, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    x = torch.randn(200, 2048, generator=g).to(torch.bfloat16).to(dev)
     wp = pkg.ops.pack_bf16_weight(w)
-    full = pkg.ops.bf16_decode_linear(x, wp, 3000)
-    for lo, hi in ((1, 16), (17, 32), (33, 64)):
-        part = pkg.ops.bf16_decode_linear(x[:lo], wp, 3000)
-        assert torch.equal(part, pkg.ops.bf16_decode_linear(x[:hi], wp, 3000)[:lo])
-    assert torch.equal(full, pkg.ops.bf16_decode_linear(x, wp, 3000))
+    full = pkg.ops.bf16_decode_linear(x, wp, n)
+    for lo, hi in ((1, 16), (17, 32), (33, 64), (65, 200)):
+        part = pkg.ops.bf16_decode_linear(x[:lo], wp, n)
+        assert torch.equal(part, pkg.ops.bf16_decode_linear(x[:hi], wp, n)[:lo])
+    assert torch.equal(full, pkg.ops.bf16_decode_linear(x, wp, n))

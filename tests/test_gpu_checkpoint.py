@@ -37,6 +37,28 @@ def test_round_trip_is_bit_identical(pkg, dev, tmp_path, mode):
         assert isinstance(layer.mlp, pkg.Int8GluMLP)
         assert isinstance(layer.self_attn.q_proj, pkg.Int8Linear)
         assert layer.self_attn.q_proj.mode == mode
+    assert isinstance(loaded.lm_head, pkg.PackedBf16Linear)
+    with torch.no_grad():
+        got = loaded(ids).logits
+    assert torch.equal(got, ref)
+
+
+def test_round_trip_with_tied_embeddings(pkg, dev, tmp_path):
+    """A tied lm_head (Llama-3.2's tie_word_embeddings) is stored once, as the embedding, and
+    comes back packed from it: bit-identical logits."""
+    from safetensors import safe_open
+
+    model = pkg.quantize_model_(_llama(dev, 3, tie_word_embeddings=True), "int8")
+    assert isinstance(model.lm_head, pkg.PackedBf16Linear)
+    assert torch.equal(model.lm_head.unpacked_weight(), model.model.embed_tokens.weight)
+    ids = torch.randint(0, 96, (1, 10), device=dev)
+    with torch.no_grad():
+        ref = model(ids).logits
+    path = pkg.save_int8_checkpoint(model, tmp_path / "t.safetensors")
+    with safe_open(str(path), "pt") as f:
+        assert not any(k.startswith("lm_head.") for k in f.keys())
+    loaded = pkg.load_int8_checkpoint(path, dev)
+    assert isinstance(loaded.lm_head, pkg.PackedBf16Linear)
     with torch.no_grad():
         got = loaded(ids).logits
     assert torch.equal(got, ref)

@@ -99,6 +99,7 @@ def test_quantize_model_swaps_llama_projections(pkg, dev):
     ids = torch.randint(0, 64, (1, 12), device=dev)
     with torch.no_grad():
         ref_logits = model(ids).logits.float()
+    head_weight = model.lm_head.weight.detach().clone()
     pkg.quantize_model_(model, "int8")
     for layer in model.model.layers:
         for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
@@ -106,12 +107,43 @@ def test_quantize_model_swaps_llama_projections(pkg, dev):
         assert isinstance(layer.mlp, pkg.Int8GluMLP)
         assert isinstance(layer.mlp.gate_up, pkg.Int8GateUp)
         assert isinstance(layer.mlp.down_proj, pkg.Int8Linear)
-    assert isinstance(model.lm_head, nn.Linear) and not isinstance(model.lm_head, pkg.Int8Linear)
+    assert isinstance(model.lm_head, pkg.PackedBf16Linear)  # bf16, in the packed tile layout
+    assert torch.equal(model.lm_head.unpacked_weight(), head_weight)
     assert next(model.parameters()).dtype == torch.bfloat16
     with torch.no_grad():
         logits = model(ids).logits.float()
     err = (logits - ref_logits).abs().max().item()
     assert err <= 0.05 * ref_logits.abs().max().item(), err
+
+
+@pytest.mark.parametrize("m", [1, 24, 64, 100])
+def test_packed_lm_head_is_a_drop_in(pkg, dev, m):
+    """PackedBf16Linear against the bf16 nn.Linear it replaces: within the W8A16 tolerance of the
+    fp64 product (both are bf16 products with fp32 sums, in different orders), the same bits as
+    the op it wraps, and refusals for what it cannot hold."""
+    import numpy as np
+
+    from helpers import bf16_bits
+    from oracle import numerics as ora
+
+    g = torch.Generator(device="cpu").manual_seed(m)
+    lin = nn.Linear(1040, 16400, bias=False, dtype=torch.bfloat16).to(dev)
+    with torch.no_grad():
+        lin.weight.copy_((torch.randn(16400, 1040, generator=g) * 0.02).to(torch.bfloat16))
+    head = pkg.PackedBf16Linear.from_linear(lin)
+    x = torch.randn(1, m, 1040, generator=g).to(torch.bfloat16).to(dev)
+    y = head(x)
+    assert y.shape == (1, m, 16400) and y.dtype == torch.bfloat16
+    golden = (x[0].double() @ lin.weight.detach().double().t()).cpu().numpy()
+    ok, msg = ora.within_tolerance(bf16_bits(y[0]), golden)
+    assert ok, msg
+    assert torch.equal(y[0], pkg.ops.bf16_decode_linear(x[0], head.wp, 16400))
+    assert np.array_equal(head.unpacked_weight().cpu().view(torch.int16).numpy(),
+                          lin.weight.detach().cpu().view(torch.int16).numpy())
+    with pytest.raises(RuntimeError, match="bias"):
+        pkg.PackedBf16Linear.from_linear(nn.Linear(64, 16, dtype=torch.bfloat16, device=dev))
+    with pytest.raises(RuntimeError, match="bf16"):
+        pkg.PackedBf16Linear.from_linear(nn.Linear(64, 16, bias=False, device=dev))
 
 
 def test_load_time_refusals(pkg, dev):

@@ -102,6 +102,22 @@ def test_unpack_inverts_the_oracle_packing(pkg):
         np.testing.assert_array_equal(pkg.ops.unpack_weight(qp, n, k).numpy(), q)
 
 
+def test_unpack_bf16_inverts_the_oracle_packing(pkg):
+    """The packed lm_head's host-side unpack (torch views) against the oracle's bf16 packing,
+    with padding rows and K columns."""
+    import numpy as np
+
+    from oracle import numerics as ora
+
+    rng = np.random.default_rng(5)
+    for n, k in ((1, 16), (37, 80), (64, 256)):
+        w = rng.integers(0, 1 << 16, (n, k)).astype(np.uint16)
+        wp = torch.from_numpy(ora.pack_bf16_weight(w).view(np.int16)).view(torch.bfloat16)
+        wp = wp.reshape(pkg.ops.packed_bf16_shape(n, k))
+        got = pkg.ops.unpack_bf16_weight(wp, n, k).view(torch.int16).numpy().view(np.uint16)
+        np.testing.assert_array_equal(got, w)
+
+
 def test_unpack_glu_inverts_the_oracle_packing(pkg):
     import numpy as np
 
