@@ -182,6 +182,13 @@ __host__ __device__ constexpr int vmcnt_imm(int n) {
   return (n & 15) | 0x70 | 0xF00 | ((n >> 4) << 14);
 }
 
+// The same with lgkmcnt = 0: also waits for every LDS read the wave has issued. Before a raw
+// s_barrier that releases direct-to-LDS loads into a slot this wave was reading, the reads must
+// have completed, not only issued (the compiler may place the barrier above outstanding reads).
+__host__ __device__ constexpr int vmcnt_lgkm0_imm(int n) {
+  return (n & 15) | 0x70 | ((n >> 4) << 14);
+}
+
 typedef __attribute__((address_space(3))) void* LdsPtr;
 
 // Direct-to-LDS 16-byte buffer load: lane l's 16 bytes from `offset` land at lds + 16 l (lds is
