@@ -323,9 +323,8 @@ tiled_gemm_kernel(TiledArgs a) {
         const int kt = kt0 + i;
         // This wave's loads of stage kt landed (the NST-2 later stages may still be in flight)
         // and its reads of slot (i - 1) completed; after the barrier every wave's have, so the
-        // loads below may overwrite slot (i - 1). Waiting for the reads here (lgkmcnt 0) also
-        // measured 0-10 % faster on MI355X than letting the barrier pass them (W8A16 down_proj
-        // at M = 512: 98.8 -> 91.9 us; two shapes 2-3 % slower).
+        // loads below may overwrite slot (i - 1). Waiting for the reads here (lgkmcnt 0) costs
+        // 0-2 % on MI355X against letting the barrier pass reads still in flight.
         __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm((NST - 2) * LOADS));
         __builtin_amdgcn_s_barrier();
         load_x(kt + NST - 1, (i + NST - 1) % NST);
