@@ -68,6 +68,7 @@ struct PagedAttnArgs {
   uint16_t* o;  // bf16, same indexing as q with strides so_h, so_t
   int64_t so_h, so_t;
   int entries, H, HKV, G, block_size, max_q_len;
+  int bs_shift;      // log2(block_size) when it is a power of two, else -1
   int tq;            // query tokens per tile: floor(16 / G)
   int qtiles;        // ceil(max_q_len / tq)
   int parts;         // 1: a workgroup folds every chunk of its item; > 1: one chunk per workgroup
@@ -124,8 +125,8 @@ __device__ __forceinline__ uint4 attn_out8(float L, const float (&O)[8]) {
 }
 
 // NT: K and V stream with the nt cache policy; used when each K/V row is read by one workgroup
-// only (one query tile: decode).
-template <int D, bool NT>
+// only (one query tile: decode). POW2: block_size is a power of two (a shift finds a key's block).
+template <int D, bool NT, bool POW2>
 __global__ void __launch_bounds__(64 * kAttnWaves)
 paged_attn_kernel(PagedAttnArgs a) {
   static_assert(D == 128, "head_dim 128: 16 chunks of 16 bytes per K/V row");
@@ -137,6 +138,9 @@ paged_attn_kernel(PagedAttnArgs a) {
   static_assert(KT * VROWB == 16 * D * 4, "the V tile and the O tile share one LDS region");
   __shared__ __attribute__((aligned(16))) unsigned char vbuf[W][KT * VROWB];
   __shared__ float mbuf[W][16], lbuf[W][16];
+  // The pool blocks of the current chunk's positions (block_table entries b0 .. b0 + count - 1),
+  // read once per chunk so a key's address needs no dependent global load.
+  __shared__ int blk_lds[kAttnChunk + 1];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -193,23 +197,25 @@ paged_attn_kernel(PagedAttnArgs a) {
   for (int c = c_first; c < c_end; ++c) {
     const int pstart = c * kAttnChunk;
     const int pend = min(pstart + kAttnChunk, end_n);
+    auto blk_of = [&](int n) { return POW2 ? n >> a.bs_shift : n / bs; };
+    const int b0 = blk_of(pstart);
+    {
+      const int count = pend > pstart ? blk_of(pend - 1) - b0 + 1 : 0;
+      for (int i = threadIdx.x; i < count; i += 64 * W) blk_lds[i] = bt[b0 + i];
+      __syncthreads();
+    }
     // Element offset of key n's row (this K/V head) in the pool; keys past the chunk are clamped
     // to its last key, so every load stays inside the entry's own blocks.
     auto row_off = [&](int n) -> int64_t {
       n = min(n, pend - 1);
-      const int blk = bt[n / bs];
-      return (int64_t)blk * a.sb + (int64_t)(n - (n / bs) * bs) * a.sw + (int64_t)kvh * a.sh;
+      const int bi = blk_of(n);
+      return (int64_t)blk_lds[bi - b0] * a.sb + (int64_t)(n - bi * bs) * a.sw +
+             (int64_t)kvh * a.sh;
     };
-
-    float m_run = NEG_INF, l_run = 0.0f;
-    f32x4 oacc[DT];
-#pragma unroll
-    for (int t = 0; t < DT; ++t) oacc[t] = f32x4{0, 0, 0, 0};
-
-    for (int n0 = pstart + KT * wave; n0 < pend; n0 += KT * W) {
-      // K rows of the tile's two 16-key blocks (A operand) and the V tile (16 bytes x 8 per lane:
-      // row (lane / 16) + 4 i, chunk lane % 16), all issued before any use.
-      uint4 kf[2][KK], vr[8];
+    // K rows of a tile's two 16-key blocks (A operand) and its V tile (16 bytes x 8 per lane:
+    // row (lane / 16) + 4 i, chunk lane % 16).
+    uint4 kf[2][KK], vr[8];
+    auto load_k = [&](int n0) {
 #pragma unroll
       for (int bk = 0; bk < 2; ++bk) {
         const uint16_t* kp = a.k_pool + row_off(n0 + 16 * bk + n16) + 8 * grp;
@@ -218,12 +224,32 @@ paged_attn_kernel(PagedAttnArgs a) {
           kf[bk][kk] =
               NT ? load16_stream(kp + 32 * kk) : *reinterpret_cast<const uint4*>(kp + 32 * kk);
       }
+    };
+    auto load_v = [&](int n0) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const uint16_t* vp = a.v_pool + row_off(n0 + grp + 4 * i) + 8 * n16;
         vr[i] = NT ? load16_stream(vp) : *reinterpret_cast<const uint4*>(vp);
       }
+    };
 
+    float m_run = NEG_INF, l_run = 0.0f;
+    f32x4 oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[t] = f32x4{0, 0, 0, 0};
+
+    // Each wave's tiles n0 = pstart + KT wave + KT W j. The next tile's K rows are loaded as soon
+    // as the scores have consumed this tile's, and its V rows once this tile's are in LDS, so
+    // they travel during this tile's softmax and P V. After the last tile these loads read the
+    // chunk's last key again (row_off clamps), which keeps them unconditional and their waits
+    // exact.
+    if (pstart + KT * wave < pend) {
+      load_k(pstart + KT * wave);
+      // K before V, as in the loop, so the scores wait for K alone.
+      __builtin_amdgcn_sched_barrier(0);
+      load_v(pstart + KT * wave);
+    }
+    for (int n0 = pstart + KT * wave; n0 < pend; n0 += KT * W) {
       // Scores: lane holds keys n0 + 16 bk + 4 grp + r of row n16.
       f32x4 st[2];
 #pragma unroll
@@ -233,6 +259,7 @@ paged_attn_kernel(PagedAttnArgs a) {
         for (int kk = 0; kk < KK; ++kk)
           st[bk] = mfma16x16x32(as_bf16x8(kf[bk][kk]), qf[kk], st[bk]);
       }
+      load_k(n0 + KT * W);
       float s[8];
       float tmax = NEG_INF;
 #pragma unroll
@@ -276,6 +303,7 @@ paged_attn_kernel(PagedAttnArgs a) {
         const int rr = grp + 4 * i;
         *reinterpret_cast<uint4*>(vb + rr * VROWB + 16 * (n16 ^ (2 * (rr & 3)))) = vr[i];
       }
+      load_v(n0 + KT * W);
       // O += P V. Group grp reads rows kb + (n16 >> 2), kb = 4 grp (keys 0..3 of its contraction
       // slice) and 16 + 4 grp (keys 4..7), at logical columns 16 t + 4 (n16 & 3).
       const int rlo = n16 >> 2;
@@ -445,6 +473,9 @@ int launch_paged_attention(const uint16_t* q, int64_t sq_h, int64_t sq_t, const 
   a.HKV = (int)HKV;
   a.G = (int)(H / HKV);
   a.block_size = (int)block_size;
+  a.bs_shift = -1;
+  for (int s = 0; s < 31; ++s)
+    if ((int64_t)1 << s == block_size) a.bs_shift = s;
   a.max_q_len = (int)max_q_len;
   const int64_t max_ctx = max_blocks * block_size;
   const AttnPlan pl = attn_plan(a.entries, a.H, a.HKV, 128, a.max_q_len, max_ctx, attn_cus());
@@ -458,8 +489,13 @@ int launch_paged_attention(const uint16_t* q, int64_t sq_h, int64_t sq_t, const 
   const int64_t blocks = (int64_t)a.entries * a.HKV * pl.qtiles * pl.parts;
   if (blocks > 0x7fffffff) return LSE_E_RANGE;
   void* args[] = {&a};
-  const void* fn = pl.qtiles == 1 ? reinterpret_cast<const void*>(&paged_attn_kernel<128, true>)
-                                  : reinterpret_cast<const void*>(&paged_attn_kernel<128, false>);
+  const bool pow2 = a.bs_shift >= 0;
+  const void* fn =
+      pl.qtiles == 1
+          ? (pow2 ? reinterpret_cast<const void*>(&paged_attn_kernel<128, true, true>)
+                  : reinterpret_cast<const void*>(&paged_attn_kernel<128, true, false>))
+          : (pow2 ? reinterpret_cast<const void*>(&paged_attn_kernel<128, false, true>)
+                  : reinterpret_cast<const void*>(&paged_attn_kernel<128, false, false>));
   hipError_t err = hipLaunchKernel(fn,
                                    dim3((unsigned)blocks), dim3(64 * kAttnWaves), args, 0, stream);
   if (err == hipSuccess && pl.parts > 1) {
