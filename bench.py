@@ -72,7 +72,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true", help="skip prefill and W8A8 figures")
     p.add_argument("--only", choices=["decode", "prefill", "w8a8", "glu", "attention",
-                                      "lm-head", "decode-step"],
+                                      "lm-head", "decode-step", "tp8"],
                    help="one family; decode-step is config 4 (a 32-layer model's decode step)")
     p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
                    help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
@@ -422,6 +422,69 @@ def bench_glu(pkg, dev, steps: int, gen) -> dict:
                             "mfma_frac": round(4 * m * i * k / t / 1e12 / BF16_PEAK_TFLOPS, 4),
                             "unfused_us": round(t0 * 1e6, 1)}
     return res
+
+
+TP8_SHARDS = [("qkv", 4096, 768), ("o_proj", 512, 4096), ("gate_up", 4096, 3584),
+              ("down", 1792, 4096)]  # (name, K, N) of one GPU's share at tensor parallelism 8
+
+
+def bench_tp8_shards(pkg, dev, steps: int, gen) -> dict:
+    """One GPU's share of each Llama-3-8B projection under 8-way tensor parallelism (column-
+    parallel qkv and gate_up split N, row-parallel o_proj and down split K; the all-reduce of the
+    row-parallel outputs is not timed): W8A16 decode GB/s at M = 1 and 64 and prefill TFLOP/s at
+    M = 2048, each over enough rotated weight copies (at least 768 MB) that every launch streams
+    its weight from HBM, replayed from graphs."""
+    import torch
+
+    res = {}
+    for name, k, n in TP8_SHARDS:
+        copies = make_weights(pkg, dev, k, n, -(-768_000_000 // (k * n)), gen)
+        row = {}
+        for m in (1, 64, 2048):
+            x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+
+            def step(x=x):
+                for q, s in copies:
+                    pkg.ops.w8a16_linear(x, q, s)
+
+            t = time_graph(step, steps) / len(copies)
+            if m == 2048:
+                row["M2048_tflops"] = round(2.0 * m * n * k / t / 1e12, 1)
+            else:
+                row[f"M{m}_us"] = round(t * 1e6, 2)
+                row[f"M{m}_gbps"] = round(decode_bytes(m, k, n) / t / 1e9, 1)
+        res[f"{name}_{k}x{n}"] = row
+        del copies
+    return res
+
+
+def device_peaks() -> dict:
+    """The roofline peaks used (AMD's published MI355X figures) beside the ones re-derived on this
+    box: CUs x max engine clock (rocminfo) x per-CU dense rate (bf16: 4 SIMDs x 1024 flops per
+    clock, the 16x16x32 MFMA's 16 K flops per 16 cycles; int8 twice that)."""
+    import re
+    import subprocess
+
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    cus = props.multi_processor_count
+    mhz = None
+    try:
+        info = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60).stdout
+        gpu = info[info.find(getattr(props, "gcnArchName", "gfx950").split(":")[0]):]
+        m = re.search(r"Max Clock Freq\. \(MHz\):\s*(\d+)", gpu)
+        mhz = int(m.group(1)) if m else None
+    except (OSError, subprocess.SubprocessError):
+        pass
+    out = {"name": props.name, "arch": getattr(props, "gcnArchName", None), "cus": cus,
+           "max_engine_clock_mhz": mhz, "published": {"hbm_gbps": HBM_PEAK_GBPS,
+                                                       "bf16_tflops": BF16_PEAK_TFLOPS,
+                                                       "int8_tops": INT8_PEAK_TOPS}}
+    if mhz:
+        out["derived"] = {"bf16_tflops": round(cus * mhz * 1e6 * 4096 / 1e12, 1),
+                          "int8_tops": round(cus * mhz * 1e6 * 8192 / 1e12, 1)}
+    return out
 
 
 def bench_lm_head(pkg, dev, steps: int, gen) -> dict:
@@ -1142,6 +1205,10 @@ def main() -> None:
     if args.only == "decode-step":
         print(json.dumps({"decode_step": bench_decode_step(pkg, dev, args.steps)}))
         return
+    if args.only == "tp8":
+        print(json.dumps({"tp8_shard_shapes": bench_tp8_shards(pkg, dev, args.steps, gen),
+                          "device": device_peaks()}))
+        return
 
     secondary = {}
     if not args.no_secondary and args.only is None:
@@ -1152,8 +1219,10 @@ def main() -> None:
         secondary["decode_vs_reference_bf16"] = bench_decode_reference(
             dev, args.steps, gen, dec["seconds_per_step"])
         secondary["eager_int8_linear"] = bench_eager_overhead(pkg, dev, args.steps, gen)
+        secondary["tp8_shard_shapes"] = bench_tp8_shards(pkg, dev, args.steps, gen)
         torch.cuda.empty_cache()
         secondary["decode_step"] = bench_decode_step(pkg, dev, args.steps)
+        secondary["device"] = device_peaks()
 
     cpu = cpu_int8 = None
     if not args.no_cpu and args.only is None:
