@@ -57,6 +57,7 @@ PROFILE_PREFILL = REPO_ROOT / "profiles" / "tiled_gemm_kernel_prefill.md"
 PROFILE_W8A8 = REPO_ROOT / "profiles" / "tiled_gemm_kernel_w8a8.md"
 PROFILE_GLU = REPO_ROOT / "profiles" / "fused_gate_up_kernels.md"
 PROFILE_ATTN = REPO_ROOT / "profiles" / "paged_attn_kernel_decode.md"
+PROFILE_HEAD = REPO_ROOT / "profiles" / "bf16_lm_head_kernels.md"
 CUS, SIMDS_PER_CU, XCDS = 256, 4, 8
 
 
@@ -79,6 +80,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--summarize-attention", metavar="TRACE",
                    help="write the paged attention profile summary from a kernel trace of "
                         "--only attention")
+    p.add_argument("--summarize-lm-head", metavar="TRACE",
+                   help="write the packed bf16 lm_head profile summary from a kernel trace of "
+                        "--only lm-head --steps 5")
     p.add_argument("--summarize-glu", metavar="TRACE",
                    help="write the fused gate_up profile summary from a kernel trace of --only glu")
     p.add_argument("--summarize-w8a8", nargs=2, metavar=("TRACE", "PMC"),
@@ -499,7 +503,7 @@ def bench_lm_head(pkg, dev, steps: int, gen) -> dict:
     ws = [(torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(dev) for _ in range(2)]
     wps = [pkg.ops.pack_bf16_weight(w) for w in ws]
     res = {}
-    for m in DECODE_MS + [128, 256]:
+    for m in LM_HEAD_MS:
         x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
         ours = lambda x=x: [pkg.ops.bf16_decode_linear(x, wp, n) for wp in wps]  # noqa: E731
         blas = lambda x=x: [torch.nn.functional.linear(x, w) for w in ws]  # noqa: E731
@@ -907,6 +911,66 @@ def summarize_glu(trace_dir: str) -> None:
     print("\n".join(out))
 
 
+LM_HEAD_MS = DECODE_MS + [128, 256]
+
+
+def summarize_lm_head(trace_dir: str, steps: int = 5) -> None:
+    """Per-M kernel durations of `bench.py --only lm-head --steps 5` from a kernel trace: the
+    packed bf16 path (lse kernels) against the vendor BLAS's F.linear, in bench order (for each M
+    the packed path, then the vendor's; each a graph of 2 calls, run eagerly once, then
+    replayed steps + 1 times, so 2 (steps + 2) calls per block; a call may take several vendor
+    kernels)."""
+    import csv
+    import statistics
+
+    with open(Path(trace_dir) / "run_kernel_trace.csv", newline="") as f:
+        trace = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    blocks: list[list[dict]] = []
+    for r in trace:
+        # The GEMM kernels only: not the packing of the two weight copies, buffer copies, or
+        # the small fills that graph capture launches.
+        name = r["Kernel_Name"]
+        if "pack_bf16" in name or not ("lse::" in name or "Cijk" in name):
+            continue
+        ours = "lse::" in name
+        if not blocks or ("lse::" in blocks[-1][0]["Kernel_Name"]) != ours:
+            blocks.append([])
+        blocks[-1].append(r)
+    calls = 2 * (steps + 2)
+    if len(blocks) != 2 * len(LM_HEAD_MS):
+        raise RuntimeError(f"{len(blocks)} kernel blocks, expected {2 * len(LM_HEAD_MS)}")
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
+    n, k = 128256, 4096
+    cmds = [
+        "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_head -o run --output-format csv -- "
+        "python3 bench.py --only lm-head --steps 5",
+        "python3 bench.py --summarize-lm-head gpurun_out/prof_head",
+    ]
+    out = [f"# Packed bf16 lm_head (N = {n}, K = {k}, 1.05 GB bf16) against the vendor BLAS, "
+           "one MI355X", "", "Commands (repository root, one MI355X; the last runs on any host):",
+           "", "```", *cmds, "```", "",
+           "Two weight copies rotate, so every call streams its 1.05 GB from HBM. A call's time is "
+           "the sum of its kernels' trace durations (end - start); medians over the block's "
+           f"{calls} calls. GB/s = (2NK + 2MK + 2MN) / time.", "",
+           "| M | packed kernel | packed us | packed GB/s | vendor kernels | vendor us | "
+           "vendor GB/s |", "|---|---|---|---|---|---|---|"]
+    for mi, m in enumerate(LM_HEAD_MS):
+        row = [str(m)]
+        for b in blocks[2 * mi:2 * mi + 2]:
+            per = len(b) // calls
+            if per * calls != len(b):
+                raise RuntimeError(f"M={m}: {len(b)} dispatches for {calls} calls")
+            us = statistics.median(sum(dur(r) for r in b[c * per:(c + 1) * per])
+                                   for c in range(calls))
+            names = sorted({r["Kernel_Name"].split("(")[0].replace("void ", "")
+                            .replace("lse::", "")[:70] for r in b})
+            row += [" + ".join(f"`{s}`" for s in names), f"{us:.1f}",
+                    f"{(2 * n * k + 2 * m * k + 2 * m * n) / us / 1e3:.0f}"]
+        out.append("| " + " | ".join(row) + " |")
+    PROFILE_HEAD.write_text("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
 def summarize_attention(trace_dir: str) -> None:
     """Kernel-trace durations of `bench.py --only attention`: the paged_attn_kernel dispatches,
     in order, fall into one equal run per ATTN_CASES entry (each case dispatches the same
@@ -1165,6 +1229,9 @@ def main() -> None:
         return
     if args.summarize_glu:
         summarize_glu(args.summarize_glu)
+        return
+    if args.summarize_lm_head:
+        summarize_lm_head(args.summarize_lm_head)
         return
     if args.summarize_attention:
         summarize_attention(args.summarize_attention)
