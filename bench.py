@@ -462,6 +462,42 @@ def bench_tp8_shards(pkg, dev, steps: int, gen) -> dict:
     return res
 
 
+def bench_launch_floor(pkg, dev, steps: int, gen) -> dict:
+    """The fixed cost of one kernel in a graph, which bounds the small decode shapes: 64
+    back-to-back launches replayed from one graph, per launch, for torch's smallest elementwise
+    kernel (an in-place add on 16 floats) and for the decode GEMM on a trivial shape (M = 1,
+    K = 64, N = 16: one K step, one row tile) and on a 64 KB weight (K = 4096, N = 16: 64 K
+    steps over the workgroup's 8 waves)."""
+    import torch
+
+    res = {}
+    a = torch.zeros(16, device=dev)
+
+    def add():
+        for _ in range(64):
+            a.add_(1.0)
+
+    res["torch_elementwise_us"] = round(time_graph(add, steps) / 64 * 1e6, 2)
+    lib = pkg.library()
+    for k, n in ((64, 16), (4096, 16)):
+        w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
+        q, s = pkg.ops.quantize_weight_per_channel(w)
+        qp = pkg.ops.pack_weight(q)
+        x = torch.randn(1, k, generator=gen).to(torch.bfloat16).to(dev)
+        y = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
+
+        def gemm(x=x, qp=qp, s=s, y=y, k=k, n=n):
+            stream = torch.cuda.current_stream().cuda_stream
+            for _ in range(64):
+                st = lib.lse_w8a16_gemm_algo(x.data_ptr(), k, qp.data_ptr(), s.data_ptr(),
+                                             y.data_ptr(), n, 1, n, k, 1, None, 0, stream)
+                if st:
+                    raise RuntimeError(f"lse_w8a16_gemm_algo status {st}")
+
+        res[f"decode_gemm_K{k}_N{n}_us"] = round(time_graph(gemm, steps) / 64 * 1e6, 2)
+    return res
+
+
 def device_peaks() -> dict:
     """The roofline peaks used (AMD's published MI355X figures) beside the ones re-derived on this
     box: CUs x max engine clock (rocminfo) x per-CU dense rate (bf16: 4 SIMDs x 1024 flops per
@@ -1287,6 +1323,7 @@ def main() -> None:
             dev, args.steps, gen, dec["seconds_per_step"])
         secondary["eager_int8_linear"] = bench_eager_overhead(pkg, dev, args.steps, gen)
         secondary["tp8_shard_shapes"] = bench_tp8_shards(pkg, dev, args.steps, gen)
+        secondary["launch_floor"] = bench_launch_floor(pkg, dev, args.steps, gen)
         torch.cuda.empty_cache()
         secondary["decode_step"] = bench_decode_step(pkg, dev, args.steps)
         secondary["device"] = device_peaks()
