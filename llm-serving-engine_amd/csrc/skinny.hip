@@ -232,44 +232,73 @@ skinny_kernel(SkinnyArgs a) {
       // which order like the values since they are >= 0), then every element's quant1 with the
       // row's scale, written at its swizzled position (chunk pc of row m holds logical chunk
       // pc ^ (m & xswz); K is a multiple of 16, so a 16-element chunk is wholly in or out).
+      // Work item c is physical chunk c of the staged image (16 int8 of row c / rch), i.e. 16
+      // bf16 of x (logical chunk pc ^ (m & xswz), zeros past K). A thread keeps its first QR
+      // items' x in registers between the amax pass and the quantizing pass, so x is read
+      // from memory once when it fits (M x K up to 16 x 512 x QR elements).
       if (threadIdx.x < 16) qx_amax[threadIdx.x] = 0u;
       __syncthreads();
       const uint16_t* xb = static_cast<const uint16_t*>(a.x);
-      const int kch = a.K / 8;
-      for (int c = threadIdx.x; c < a.M * kch; c += 64 * W) {
-        const int m = c / kch, k8 = 8 * (c - m * kch);
-        const uint4 v = *reinterpret_cast<const uint4*>(xb + (int64_t)m * a.ldx + k8);
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-        float mx = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          mx = fmaxf(mx, fabsf(__builtin_bit_cast(float, w4[j] << 16)));
-          mx = fmaxf(mx, fabsf(__builtin_bit_cast(float, w4[j] & 0xffff0000u)));
-        }
-        atomicMax(&qx_amax[m], __builtin_bit_cast(unsigned, mx));
-      }
-      __syncthreads();
       const int rch = xrow_bytes / 16;  // 16-byte chunks per staged row
-      for (int c = threadIdx.x; c < a.M * rch; c += 64 * W) {
+      const int items = a.M * rch;
+      auto load_item = [&](int c, uint4& v0, uint4& v1) {
         const int m = c / rch, pc = c - m * rch;
         const int k16 = 16 * (pc ^ (m & xswz));
-        const float scale = row_scale(__builtin_bit_cast(float, qx_amax[m]));
-        uint32_t packed[4] = {0, 0, 0, 0};
+        v0 = v1 = make_uint4(0, 0, 0, 0);
         if (k16 < a.K) {
           const uint16_t* src = xb + (int64_t)m * a.ldx + k16;
-          const uint4 v0 = *reinterpret_cast<const uint4*>(src);
-          const uint4 v1 = *reinterpret_cast<const uint4*>(src + 8);
-          const uint32_t w8[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, w8[j] << 16), scale);
-            const uint32_t hi =
-                (uint8_t)quant1(__builtin_bit_cast(float, w8[j] & 0xffff0000u), scale);
-            packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
-          }
+          v0 = *reinterpret_cast<const uint4*>(src);
+          v1 = *reinterpret_cast<const uint4*>(src + 8);
         }
-        *reinterpret_cast<uint4*>(x_lds + 16 * c) = make_uint4(packed[0], packed[1], packed[2],
-                                                                packed[3]);
+      };
+      auto amax_item = [&](int c, const uint4& v0, const uint4& v1) {
+        const uint32_t w8[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          mx = fmaxf(mx, fabsf(__builtin_bit_cast(float, w8[j] << 16)));
+          mx = fmaxf(mx, fabsf(__builtin_bit_cast(float, w8[j] & 0xffff0000u)));
+        }
+        atomicMax(&qx_amax[c / rch], __builtin_bit_cast(unsigned, mx));
+      };
+      auto quant_item = [&](int c, const uint4& v0, const uint4& v1) {
+        const float scale = row_scale(__builtin_bit_cast(float, qx_amax[c / rch]));
+        const uint32_t w8[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        uint32_t packed[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, w8[j] << 16), scale);
+          const uint32_t hi = (uint8_t)quant1(__builtin_bit_cast(float, w8[j] & 0xffff0000u), scale);
+          packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
+        }
+        *reinterpret_cast<uint4*>(x_lds + 16 * c) =
+            make_uint4(packed[0], packed[1], packed[2], packed[3]);
+      };
+      constexpr int QR = 2;
+      uint4 kv0[QR], kv1[QR];
+#pragma unroll
+      for (int it = 0; it < QR; ++it) {
+        const int c = threadIdx.x + 64 * W * it;
+        if (c < items) {
+          load_item(c, kv0[it], kv1[it]);
+          amax_item(c, kv0[it], kv1[it]);
+        }
+      }
+      for (int c = threadIdx.x + 64 * W * QR; c < items; c += 64 * W) {
+        uint4 v0, v1;
+        load_item(c, v0, v1);
+        amax_item(c, v0, v1);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < QR; ++it) {
+        const int c = threadIdx.x + 64 * W * it;
+        if (c < items) quant_item(c, kv0[it], kv1[it]);
+      }
+      for (int c = threadIdx.x + 64 * W * QR; c < items; c += 64 * W) {
+        uint4 v0, v1;
+        load_item(c, v0, v1);
+        quant_item(c, v0, v1);
       }
       sxv[0] = r16 < a.M ? row_scale(__builtin_bit_cast(float, qx_amax[r16])) : 0.0f;
     }

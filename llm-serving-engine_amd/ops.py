@@ -275,17 +275,25 @@ def w8a8_gemm(
     return y, acc
 
 
+ONE_LAUNCH_W8A8_MAX_ROWS = 2  # rows up to which w8a8_linear takes the one-launch kernel
+
+
 def w8a8_linear(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor,
-                want_acc: bool = False):
+                want_acc: bool = False, one_launch: bool | None = None):
     """Dynamic per-token W8A8: quantize x per row, int8 GEMM with exact int32 accumulation,
     y = bf16((acc * sx[m]) * s[n]). x (..., K) bf16 → y (..., N) bf16 (with want_acc, also the
-    (M, N) int32 accumulators). Small decode batches run as one kernel that quantizes while it
-    stages x (`lse_w8a8_linear`); others quantize first, then run the GEMM. Both give the same
-    bits."""
+    (M, N) int32 accumulators). One or two rows run as one kernel that quantizes while it
+    stages x (`lse_w8a8_linear`); more rows quantize first, then run the GEMM. Both give the same
+    bits. The one-launch kernel quantizes all of x in every workgroup, which from 4 rows up costs
+    more than the second launch saves (measured on MI355X over the Llama-3-8B shapes: 6-17 %
+    faster at 1 row, mostly faster at 2, 5-80 % slower from 4 to 16). `one_launch` True takes
+    the one-launch kernel wherever it runs (`lse_w8a8_linear_supported`), False never."""
     n, k = scales.shape[0], x.shape[-1]
     lib = _lib.library()
     m = x.numel() // k if k else 0
-    if m and lib.lse_w8a8_linear_supported(m, k):
+    if one_launch is None:
+        one_launch = m <= ONE_LAUNCH_W8A8_MAX_ROWS
+    if m and one_launch and lib.lse_w8a8_linear_supported(m, k):
         dev = _on_gpu(x, qp, scales)
         _require(x.dtype == torch.bfloat16, f"W8A8 expects bf16 activations, got {x.dtype}")
         _require(scales.dtype == torch.float32 and scales.dim() == 1, "scales must be fp32 (N,)")

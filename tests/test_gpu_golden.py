@@ -72,7 +72,8 @@ def test_w8a8_one_launch_matches_the_fixture(pkg, dev, case):
     """The decode kernel that quantizes x while staging it (lse_w8a8_linear), from bf16."""
     qp = pkg.ops.pack_weight(torch.from_numpy(case["q"]).to(dev))
     y, acc = pkg.ops.w8a8_linear(to_bf16_tensor(case["xo"], dev), qp,
-                                 torch.from_numpy(case["s"]).to(dev), want_acc=True)
+                                 torch.from_numpy(case["s"]).to(dev), want_acc=True,
+                                 one_launch=True)
     np.testing.assert_array_equal(acc.cpu().numpy(), case["acc"])
     np.testing.assert_array_equal(bf16_bits(y), case["y_w8a8"])
 

@@ -148,7 +148,7 @@ def test_fused_linear_bit_exact(pkg, dev, m, n, k):
     x = to_bf16_tensor(x_bits, dev)
     qp = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
     st = torch.from_numpy(s).to(dev)
-    y, acc = pkg.ops.w8a8_linear(x, qp, st, want_acc=True)
+    y, acc = pkg.ops.w8a8_linear(x, qp, st, want_acc=True, one_launch=True)
     torch.cuda.synchronize()
     xq_ref, sx_ref = ora.quantize_act_per_token(x_bits)
     acc_ref = ora.w8a8_accumulate(xq_ref, q)
@@ -171,7 +171,8 @@ def test_fused_linear_deep_k_and_strided_rows(pkg, dev):
     wide[:, :k] = x_bits
     x = to_bf16_tensor(wide, dev)[:, :k]
     qp = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
-    y, acc = pkg.ops.w8a8_linear(x, qp, torch.from_numpy(s).to(dev), want_acc=True)
+    y, acc = pkg.ops.w8a8_linear(x, qp, torch.from_numpy(s).to(dev), want_acc=True,
+                                 one_launch=True)
     torch.cuda.synchronize()
     xq_ref, sx_ref = ora.quantize_act_per_token(x_bits)
     acc_ref = ora.w8a8_accumulate(xq_ref, q)
