@@ -12,10 +12,11 @@
  *
  * Conventions shared by every entry point:
  *  - All pointers are device pointers. The caller owns every buffer; the library keeps no state
- *    beyond its compiled kernels and allocates nothing. The decode GEMMs of some shapes add
- *    partial sums of K ranges in a second pass through a caller-provided workspace of
- *    lse_workspace_bytes(...) bytes (0 for most calls); a workspace may be reused by calls that
- *    are ordered on one stream, never by calls that can overlap.
+ *    beyond its compiled kernels and allocates nothing. The GEMMs of some shapes (deep decode
+ *    shapes, and 65..256 tokens over a narrow weight) add partial sums of K ranges in a second
+ *    pass through a caller-provided workspace of lse_workspace_bytes(...) bytes (0 for most
+ *    calls); a workspace may be reused by calls that are ordered on one stream, never by calls
+ *    that can overlap.
  *  - Weights travel in the packed tile layout written by lse_pack_weight: tiles of 16 rows x 64
  *    K-bytes, 1 KB each, tile (rb, j) at byte (rb * ceil(K/64) + j) * 1024, its byte 16*l + i
  *    holding q[16*rb + l%16][64*j + 16*(l/16) + i], zero past N and K. One 128-bit load per lane
@@ -29,11 +30,11 @@
  *    (nothing was launched); a positive hipError_t from the launch otherwise.
  *  - Results are deterministic: no atomics, and the summation order of every output element
  *    depends only on N, K, the device's CU count and the token class of the call (M <= 16,
- *    17..32, 33..64, > 64), never on M inside the class, on other rows or on timing. Row m of y
- *    is therefore bit-identical whether it is computed alone or inside a padded batch of the
- *    same class. The classes align with power-of-two decode buckets (bucket(M) <= 16 exactly
- *    when M <= 16, and so on), so a graphed bucket and the eager batch it stands for compute
- *    each row identically.
+ *    17..32, 33..64, 65..128, 129..256, > 256), never on M inside the class, on other rows or on
+ *    timing. Row m of y is therefore bit-identical whether it is computed alone or inside a
+ *    padded batch of the same class. The classes align with power-of-two decode buckets
+ *    (bucket(M) <= 16 exactly when M <= 16, and so on), so a graphed bucket and the eager batch
+ *    it stands for compute each row identically.
  */
 #ifndef LSE_INT8_H
 #define LSE_INT8_H
@@ -79,7 +80,7 @@ enum lse_query_key {
   LSE_Q_NOALLOC_SCRATCH = 5, /* bytes of the static scratch lse_w8a16_gemm_noalloc works in */
 };
 
-#define LSE_ABI_VERSION 10
+#define LSE_ABI_VERSION 11
 #define LSE_NOALLOC_SCRATCH_BYTES (16 << 20)
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64

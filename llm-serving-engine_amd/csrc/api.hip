@@ -29,11 +29,13 @@ bool w8a8_quantizing_supported(int64_t M, int64_t K);
 int launch_w8a8_skinny_quantizing(const uint16_t* x, int64_t ldx, const int8_t* qp,
                                   const float* s, uint16_t* y, int64_t ldy, int32_t* acc,
                                   int64_t M, int64_t N, int64_t K, hipStream_t stream);
+int64_t tiled_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K);
 int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* q, const float* s, uint16_t* y,
-                      int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws, int64_t ws_bytes,
+                      hipStream_t stream);
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* q, const float* s,
                      uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
-                     hipStream_t stream);
+                     void* ws, int64_t ws_bytes, hipStream_t stream);
 int launch_w8a16_skinny_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
                             uint16_t* h, int64_t ldh, int64_t M, int64_t I, int64_t K,
                             hipStream_t stream);
@@ -228,11 +230,15 @@ int lse_pack_glu(const int8_t* q, int64_t I, int64_t K, int8_t* qp, void* stream
 
 int64_t lse_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
   if (M < 0 || N < 0 || K < 0 || (mode != LSE_MODE_W8A16 && mode != LSE_MODE_W8A8)) return -1;
-  // Only the decode kernel uses a workspace; shapes it rejects need none.
-  if (M == 0 || N == 0 || K == 0 || M > LSE_DECODE_MAX_M || N > kMaxRows || K > LSE_MAX_K ||
+  // Split-K partial sums: the decode kernel's (M <= 64) or the tiled kernel's (65..256 tokens
+  // over a narrow weight). The tiled kernel needs none at M <= 64, so the bound holds for either
+  // algorithm; shapes the entry points reject need none.
+  if (M == 0 || N == 0 || K == 0 || M > kMaxRows || N > kMaxRows || K > LSE_MAX_K ||
       K % LSE_K_ALIGN)
     return 0;
-  return lse::skinny_workspace_bytes(mode == LSE_MODE_W8A8, M, N, K);
+  const bool i8 = mode == LSE_MODE_W8A8;
+  return M <= LSE_DECODE_MAX_M ? lse::skinny_workspace_bytes(i8, M, N, K)
+                               : lse::tiled_workspace_bytes(i8, M, N, K);
 }
 
 int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
@@ -248,16 +254,17 @@ int lse_w8a16_gemm_algo(const void* x, int64_t ldx, const int8_t* qp, const floa
   if (int e = check_bf16_matrix(x, ldx, M, K, 8)) return e;
   if (int e = check_packed(N, K)) return e;
   if (algo == LSE_ALGO_AUTO) algo = M <= LSE_DECODE_MAX_M ? LSE_ALGO_DECODE : LSE_ALGO_PREFILL;
+  if (workspace_bytes < 0 || (workspace && !aligned(workspace, 16))) return LSE_E_WORKSPACE;
   if (algo == LSE_ALGO_DECODE) {
     // The decode kernel addresses x through a 32-bit buffer resource.
     if (((M - 1) * ldx + K) * 2 >= (int64_t)kBufferLimit) return LSE_E_RANGE;
-    if (workspace_bytes < 0 || (workspace && !aligned(workspace, 16))) return LSE_E_WORKSPACE;
     return lse::launch_w8a16_skinny((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K,
                                     workspace, workspace_bytes, st);
   }
   // The tiled kernel addresses a block's 256 rows of x through a 32-bit buffer resource.
   if (256 * ldx * 2 >= (int64_t)kBufferLimit) return LSE_E_RANGE;
-  return lse::launch_w8a16_gemm((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K, st);
+  return lse::launch_w8a16_gemm((const uint16_t*)x, ldx, qp, s, (uint16_t*)y, ldy, M, N, K,
+                                workspace, workspace_bytes, st);
 }
 
 int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* qp, const float* s, void* y,
@@ -289,14 +296,15 @@ int lse_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const flo
   if (!xq) return LSE_E_NULL;
   if (!aligned(xq, 16)) return LSE_E_ALIGN;
   if (int e = check_packed(N, K)) return e;
+  if (workspace_bytes < 0 || (workspace && !aligned(workspace, 16))) return LSE_E_WORKSPACE;
   if (M <= LSE_DECODE_MAX_M) {
     if (M * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
-    if (workspace_bytes < 0 || (workspace && !aligned(workspace, 16))) return LSE_E_WORKSPACE;
     return lse::launch_w8a8_skinny(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, workspace,
                                    workspace_bytes, st);
   }
   if (256 * K >= (int64_t)kBufferLimit) return LSE_E_RANGE;
-  return lse::launch_w8a8_gemm(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, st);
+  return lse::launch_w8a8_gemm(xq, sx, qp, s, (uint16_t*)y, ldy, acc, M, N, K, workspace,
+                               workspace_bytes, st);
 }
 
 int lse_w8a8_linear_supported(int64_t M, int64_t K) {

@@ -34,7 +34,9 @@
 // 32 x 1 strip.
 //
 // Summation order: the K steps in increasing order, two K=32 MFMAs per step (W8A16) in a fixed
-// chain per output; it depends only on K. int32 accumulation (W8A8) is exact in any order.
+// chain per output; it depends only on K, or with K splits (65..256 tokens over a narrow weight,
+// tiled_splits) on the split count too: each range's steps in order, then the ranges added in
+// order by a second pass. int32 accumulation (W8A8) is exact in any order.
 //
 // Fused gate/up (GLU): with the weight in the gate/up layout (lse_common.h) a block's first row
 // tile is even and a wave's TN row tiles are an even-aligned run, so its tiles j (even, gate) and
@@ -532,19 +534,48 @@ static int launch_tiled_range(const TiledShape& sh, bool decode, const void* x, 
   return e == hipSuccess ? launch_status() : (int)e;
 }
 
+int launch_skinny_reduce_parts(bool i8, const void* part, const float* s, const float* sx,
+                               uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N,
+                               int splits, hipStream_t stream);  // skinny.hip
+
+// K splits just above the decode range. At 65..256 tokens a narrow weight gives few tiles
+// (down_proj at M = 65: 64 tiles of 64 x 128 for 256 CUs, each over all 14336 of K), so the tiled
+// kernel splits K into S ranges whose raw partial sums the decode kernel's second pass adds in
+// split order, as the decode route does for down_proj. S depends on the token class (65..128 or
+// 129..256, each priced at its largest M with the cost model's tile), N, K and the CU count only,
+// never on M inside the class, so a row's bits do not depend on the batch around it: S rounds
+// CUs / tiles, at most 8, with at least 8 K steps per range. Gate/up (GLU) tiles never split.
+// On MI355X at 65 tokens (W8A16), against one launch over all of K: down_proj 31 us against 82,
+// o_proj 15 against 27, qkv 21 against 28.
+static int tiled_splits(bool i8, int64_t M, int64_t N, int64_t K, int cus) {
+  if (M <= LSE_DECODE_MAX_M || M > 256) return 1;
+  const int64_t cm = M <= 128 ? 128 : 256;
+  const TiledShape sh = i8 ? tiled_shape<true>(cm, N, cus) : tiled_shape<false>(cm, N, cus);
+  const int64_t tiles = ceil_div(cm, sh.bm) * ceil_div(N, sh.bn);
+  int splits = (int)std::min<int64_t>(8, std::max<int64_t>(1, (cus + tiles / 2) / tiles));
+  while (splits > 1 && ceil_div(K, kTileK) / splits < 8) --splits;
+  return splits;
+}
+
+int64_t tiled_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K) {
+  const int splits = tiled_splits(i8, M, N, K, device_cus());
+  return splits > 1 ? (int64_t)splits * M * kTileRows * ceil_div(N, kTileRows) * 4 : 0;
+}
+
 // The cost model's tile over all N, except when its tiles leave a partial last round on the CUs
 // (gate_up at M = 2048: 896 tiles of 256 x 256 for 256 CUs, 3.5 rounds) and re-tiling the
 // columns of that round fills them better: then the full rounds run as one launch and the
 // remaining columns, with the cost model's tile for them, as a second (gate_up at M = 2048: 768
 // tiles of 256 x 256, then 256 of 128 x 256 over the last 4096 rows). Every output sums its K
-// steps in increasing order whatever the tile, so the split changes no result.
+// steps in increasing order whatever the tile, so the split changes no result. K splits
+// (tiled_splits > 1, workspace `ws`) take precedence over it.
 // `wide_decode`: the 32 x 128 or 64 x 128 tile of launch_w8a16_wide_decode instead of the cost
 // model's.
 template <bool I8>
 static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const float* s,
                         const float* sx, uint16_t* y, int64_t ldy, int32_t* acc, int64_t M,
                         int64_t N, int64_t K, int64_t glu, hipStream_t stream,
-                        bool wide_decode = false) {
+                        bool wide_decode = false, void* ws = nullptr, int64_t ws_bytes = 0) {
   if (glu > 0) N = 2 * kTileRows * ceil_div(glu, kTileRows);
   if (wide_decode) {
     const TiledShape sh{(I8 || M > 32) ? 64 : 32, 128};
@@ -556,6 +587,38 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
   const TiledShape sh = tiled_shape<I8>(M, N, cus, &cost);
   const int64_t mblocks = ceil_div(M, sh.bm);
   const int64_t blocks = mblocks * ceil_div(N, sh.bn);
+  const int splits = glu > 0 ? 1 : tiled_splits(I8, M, N, K, cus);
+  if (splits > 1) {
+    if (!ws || ws_bytes < (int64_t)splits * M * kTileRows * ceil_div(N, kTileRows) * 4)
+      return LSE_E_WORKSPACE;
+    TiledArgs a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.qp = qp;
+    a.s = s;
+    a.sx = sx;
+    a.y = y;
+    a.ldy = ldy;
+    a.acc = acc;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.nsteps = (int)ceil_div(K, kTileK);
+    a.nrb = (int)ceil_div(N, kTileRows);
+    a.mblocks = (int)mblocks;
+    a.nblocks = (int)ceil_div(N, sh.bn);
+    a.splits = splits;
+    a.ssteps = (int)ceil_div(a.nsteps, splits);
+    a.part = ws;
+    void* args[] = {&a};
+    const hipError_t e =
+        hipLaunchKernel(tiled_kernel_for<I8, false>(sh, false),
+                        dim3((unsigned)(blocks * splits)),
+                        dim3(sh.bm <= 64 ? 256 : kTiledThreads), args, 0, stream);
+    if (e != hipSuccess) return (int)e;
+    if (int st = launch_status()) return st;
+    return launch_skinny_reduce_parts(I8, ws, s, sx, y, ldy, acc, M, N, splits, stream);
+  }
   const int64_t full = blocks / cus;  // whole rounds of the chosen tile
   if (!acc && full >= 1 && blocks % cus && (full * cus) % mblocks == 0) {
     const int64_t n_bulk = full * cus / mblocks * sh.bn;
@@ -577,9 +640,10 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
 }
 
 int launch_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
-                      uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                      hipStream_t stream) {
-  return launch_tiled<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, 0, stream);
+                      uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                      int64_t ws_bytes, hipStream_t stream) {
+  return launch_tiled<false>(x, ldx, qp, s, nullptr, y, ldy, nullptr, M, N, K, 0, stream, false,
+                             ws, ws_bytes);
 }
 
 // The decode kernel's 17..32- and 33..64-token classes over a wide weight (the MLP gate/up
@@ -644,10 +708,6 @@ int launch_bf16_tiled(const uint16_t* x, int64_t ldx, const uint16_t* wp, uint16
       hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(bm <= 64 ? 256 : 512), args, 0, stream);
   return e == hipSuccess ? launch_status() : (int)e;
 }
-
-int launch_skinny_reduce_parts(bool i8, const void* part, const float* s, const float* sx,
-                               uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N,
-                               int splits, hipStream_t stream);  // skinny.hip
 
 // The decode kernel's deep, narrow class at 17..64 tokens (at most 256 row tiles and at least 128
 // K steps: the MLP down projection; chosen by the decode dispatch). Tiles of the tiled kernel
@@ -722,8 +782,9 @@ int launch_w8a8_wide_decode(const int8_t* xq, const float* sx, const int8_t* qp,
 
 int launch_w8a8_gemm(const int8_t* xq, const float* sx, const int8_t* qp, const float* s,
                      uint16_t* y, int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
-                     hipStream_t stream) {
-  return launch_tiled<true>(xq, K, qp, s, sx, y, ldy, acc, M, N, K, 0, stream);
+                     void* ws, int64_t ws_bytes, hipStream_t stream) {
+  return launch_tiled<true>(xq, K, qp, s, sx, y, ldy, acc, M, N, K, 0, stream, false, ws,
+                            ws_bytes);
 }
 
 int launch_w8a16_gemm_glu(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,

@@ -124,9 +124,9 @@ def unpack_glu(qp: torch.Tensor, i: int, k: int) -> torch.Tensor:
 
 
 def workspace(mode: int, m: int, n: int, k: int, dev: torch.device) -> torch.Tensor | None:
-    """The workspace one decode-kernel call needs (some shapes add partial sums of K ranges in a
-    second pass), or None. Allocated with torch.empty, so graph-pool owned under capture; the
-    caller keeps it alive until the call is enqueued."""
+    """The workspace one GEMM call needs (deep decode shapes and 65..256 tokens over a narrow
+    weight add partial sums of K ranges in a second pass), or None. Allocated with torch.empty,
+    so graph-pool owned under capture; the caller keeps it alive until the call is enqueued."""
     nbytes = _lib.library().lse_workspace_bytes(mode, m, n, k)
     _require(nbytes >= 0, f"lse_workspace_bytes rejected (M, N, K) = ({m}, {n}, {k})")
     return torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
@@ -191,7 +191,7 @@ def w8a16_linear(
     m = x2.shape[0]
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     ldx = x2.stride(0) if m > 1 else k
-    ws = workspace(_lib.MODE_W8A16, m, n, k, dev) if algo != _lib.ALGO_PREFILL else None
+    ws = workspace(_lib.MODE_W8A16, m, n, k, dev)
     _lib.check(
         _lib.library().lse_w8a16_gemm_algo(
             x2.data_ptr(), ldx, qp.data_ptr(), scales.data_ptr(), y.data_ptr(), n,

@@ -100,10 +100,15 @@ def test_workspace_query_and_rejections(pkg):
     lib = pkg.library()
     assert lib.lse_workspace_bytes(0, -1, 64, 64) == -1
     assert lib.lse_workspace_bytes(2, 1, 64, 64) == -1
-    assert lib.lse_workspace_bytes(0, 65, 4096, 4096) == 0  # prefill kernels need none
+    assert lib.lse_workspace_bytes(0, 257, 4096, 4096) == 0  # above 256 tokens none
     assert lib.lse_workspace_bytes(1, 0, 4096, 4096) == 0
+    # 65..256 tokens over a narrow weight: the tiled kernel's K ranges, a class-wide count.
+    assert lib.lse_workspace_bytes(0, 65, 4096, 14336) > 0
+    for m in (65, 100, 128):
+        assert lib.lse_workspace_bytes(0, m, 4096, 14336) * 65 == \
+            lib.lse_workspace_bytes(0, 65, 4096, 14336) * m
     for mode in (0, 1):
-        for m in (1, 16, 17, 33, 64):
+        for m in (1, 16, 17, 33, 64, 65, 128, 129, 256):
             nbytes = lib.lse_workspace_bytes(mode, m, 4096, 14336)
             assert 0 <= nbytes <= 64 * m * (4096 + 15) and nbytes % 16 == 0
     args = (FAKE, 64, FAKE, FAKE, FAKE, 64, 2, 64, 64, 1)

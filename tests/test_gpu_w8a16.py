@@ -30,7 +30,7 @@ def _run(pkg, dev, x_bits, q, s, algo, ldy_pad=0):
     if ldy_pad:
         sentinel = torch.full((m, n + ldy_pad), -7.0, dtype=torch.bfloat16, device=dev)
         lib = pkg.library()
-        ws = pkg.ops.workspace(0, m, n, k, dev) if algo != PREFILL else None
+        ws = pkg.ops.workspace(0, m, n, k, dev)
         status = lib.lse_w8a16_gemm_algo(
             x.data_ptr(), k, qt.data_ptr(), st.data_ptr(), sentinel.data_ptr(), n + ldy_pad,
             m, n, k, algo, ws.data_ptr() if ws is not None else None,
@@ -195,12 +195,62 @@ def test_decode_rows_are_batch_invariant(pkg, dev, k, n):
         assert ora.within_tolerance(top[cls][:16], golden)[0]
 
 
-def test_prefill_rows_are_batch_invariant(pkg, dev):
-    x_bits, w = ora.seeded_inputs(32, 400, 256, 1024)
+@pytest.mark.parametrize("k,n", [(1024, 256), (14336, 512)])
+def test_prefill_rows_are_batch_invariant(pkg, dev, k, n):
+    """The tiled route's token classes (65..128 and 129..256, which may split K over a narrow
+    weight, and > 256): inside a class a row's bits do not depend on M, on the other rows or on
+    zero padding up to the class's power-of-two bucket; across classes rows agree to the
+    tolerance."""
+    x_bits, w = ora.seeded_inputs(32, 400, n, k)
     q, s = ora.quantize_weight_per_channel(w)
-    full = _run(pkg, dev, x_bits, q, s, PREFILL)
-    for m in (65, 128, 129, 257):
-        np.testing.assert_array_equal(_run(pkg, dev, x_bits[:m], q, s, PREFILL), full[:m])
+    top = {128: _run(pkg, dev, x_bits[:128], q, s, PREFILL),
+           256: _run(pkg, dev, x_bits[:256], q, s, PREFILL),
+           400: _run(pkg, dev, x_bits, q, s, PREFILL)}
+    for m, cls in ((65, 128), (100, 128), (127, 128), (129, 256), (200, 256), (255, 256),
+                   (257, 400), (300, 400)):
+        np.testing.assert_array_equal(_run(pkg, dev, x_bits[:m], q, s, PREFILL),
+                                      top[cls][:m], err_msg=f"M={m}")
+    for m, cls in ((70, 128), (150, 256)):
+        padded = x_bits[:cls].copy()
+        padded[m:] = 0
+        np.testing.assert_array_equal(_run(pkg, dev, padded, q, s, PREFILL)[:m], top[cls][:m])
+    golden = ora.w8a16_golden(x_bits[:128], q, s)
+    for cls in (128, 256, 400):
+        assert ora.within_tolerance(top[cls][:128], golden)[0]
+
+
+@pytest.mark.parametrize("m", [65, 100, 128, 129, 256])
+@pytest.mark.parametrize("n,k", [(512, 14336), (272, 4096 + 48), (4096, 1024)])
+def test_prefill_split_k(pkg, dev, m, n, k):
+    """65..256 tokens over a narrow weight: the tiled kernel splits K into up to 8 ranges whose
+    partial sums a second pass adds. (512, 14336): 8 ranges of 28 steps; (272, 4144): a ragged
+    last row tile, 65 steps in ranges of 9 with a 2-step last range ending in a 48-wide K tail;
+    (4096, 1024): 64 tiles of 64 x 128 and 2 ranges at 65..128 tokens."""
+    _check(pkg, dev, m, n, k, 5 * m + n + k, PREFILL)
+
+
+def test_prefill_rejects_a_short_workspace(pkg, dev):
+    """A split tiled shape (down_proj at 100 tokens) needs a workspace; a smaller one is refused
+    before any launch, and the decode-range bound covers either algorithm."""
+    m, n, k = 100, 4096, 14336
+    lib = pkg.library()
+    need = lib.lse_workspace_bytes(0, m, n, k)
+    assert need >= 2 * m * n * 4
+    assert lib.lse_workspace_bytes(0, m, n, k) <= 64 * m * (n + 15)
+    x = torch.zeros(m, k, dtype=torch.bfloat16, device=dev)
+    qp = torch.zeros(pkg.ops.packed_shape(n, k), dtype=torch.int8, device=dev)
+    s = torch.ones(n, dtype=torch.float32, device=dev)
+    y = torch.full((m, n), 3.0, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (x.data_ptr(), k, qp.data_ptr(), s.data_ptr(), y.data_ptr(), n, m, n, k, PREFILL)
+    assert lib.lse_w8a16_gemm_algo(*args, ws.data_ptr(), need - 16, stream) == -6
+    assert lib.lse_w8a16_gemm_algo(*args, None, 0, stream) == -6
+    torch.cuda.synchronize()
+    assert torch.all(y == 3.0)
+    assert lib.lse_w8a16_gemm_algo(*args, ws.data_ptr(), need, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.all(y == 0.0)
 
 
 def test_repeat_calls_are_deterministic(pkg, dev):
@@ -263,12 +313,13 @@ def test_llama_prefill_shapes_at_8192_tokens(pkg, dev, k, n):
 
 @pytest.mark.parametrize("k,n", LLAMA_SHAPES)
 def test_llama_prefill_shapes_full_size(pkg, dev, k, n):
-    """Config 2 at M=512 and 2048 vs torch fp32 on the GPU (8192 in the test above)."""
+    """Config 2 at M = 65, 128, 129, 256 (K split over the narrow shapes), 512 and 2048 vs torch
+    fp32 on the GPU (8192 in the test above)."""
     gen = torch.Generator(device="cpu").manual_seed(2000 + k + n)
     w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
     q, s = pkg.ops.quantize_weight_per_channel(w)
     qp = pkg.ops.pack_weight(q)
-    for m in (512, 2048):
+    for m in (65, 128, 129, 256, 512, 2048):
         x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
         y = pkg.ops.w8a16_linear(x, qp, s, algo=PREFILL)
         ref = _torch_fp32_reference(x, q, s).double().cpu().numpy()

@@ -56,6 +56,15 @@ def test_tiled_kernel_bit_exact(pkg, dev, m, n, k):
     _check(pkg, dev, m, n, k, m + n + k)
 
 
+@pytest.mark.parametrize("m", [65, 129, 256])
+@pytest.mark.parametrize("n,k", [(256, 14336), (272, 4096 + 48)])
+def test_tiled_split_k_bit_exact(pkg, dev, m, n, k):
+    """65..256 tokens over a narrow weight: K split into 8 ranges whose int32 partial sums a
+    second pass adds, with a ragged last row tile and a 2-step last range ending in a K tail
+    for (272, 4144). int32 sums are exact, so acc and y equal the oracle's bit for bit."""
+    _check(pkg, dev, m, n, k, 3 * m + n + k)
+
+
 @pytest.mark.parametrize("n,k", [(1, 16), (17, 48), (45, 1072)])
 def test_ragged_shapes_bit_exact(pkg, dev, n, k):
     for m in (1, 40, 90):
