@@ -80,8 +80,8 @@ enum lse_query_key {
   LSE_Q_NOALLOC_SCRATCH = 5, /* bytes of the static scratch lse_w8a16_gemm_noalloc works in */
 };
 
-#define LSE_ABI_VERSION 11
-#define LSE_NOALLOC_SCRATCH_BYTES (16 << 20)
+#define LSE_ABI_VERSION 12
+#define LSE_NOALLOC_SCRATCH_BYTES (32 << 20)
 #define LSE_K_ALIGN 16
 #define LSE_DECODE_MAX_M 64
 #define LSE_MAX_K 133120      /* 127*127*K < 2^31 with margin; multiple of LSE_K_ALIGN */
@@ -136,7 +136,7 @@ int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* qp, const float* s,
  * lse_w8a16_gemm without a workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls
  * no hipMalloc, hipFree or allocating routine: the workspace lse_w8a16_gemm would take lives in a
- * static device array of LSE_NOALLOC_SCRATCH_BYTES (16 MiB) that each device the library runs on
+ * static device array of LSE_NOALLOC_SCRATCH_BYTES (32 MiB) that each device the library runs on
  * holds until the process ends, its device address looked up on the device's first call. Same
  * kernels, so y is bit-identical to lse_w8a16_gemm's. Calls that overlap on one device (two
  * streams at once) share that array and race; calls in stream order do not. Returns

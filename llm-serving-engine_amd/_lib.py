@@ -53,7 +53,7 @@ MODE_W8A16, MODE_W8A8 = 0, 1
 E_WORKSPACE, E_SCRATCH = -6, -7
 Q_ABI_VERSION, Q_K_ALIGN, Q_DECODE_MAX_M, Q_MAX_K, Q_GFX_ARCH = 0, 1, 2, 3, 4
 Q_NOALLOC_SCRATCH = 5
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -542,19 +542,37 @@ int launch_skinny_reduce_parts(bool i8, const void* part, const float* s, const 
 // (down_proj at M = 65: 64 tiles of 64 x 128 for 256 CUs, each over all 14336 of K), so the tiled
 // kernel splits K into S ranges whose raw partial sums the decode kernel's second pass adds in
 // split order, as the decode route does for down_proj. S depends on the token class (65..128 or
-// 129..256, each priced at its largest M with the cost model's tile), N, K and the CU count only,
-// never on M inside the class, so a row's bits do not depend on the batch around it: S rounds
-// CUs / tiles, at most 8, with at least 8 K steps per range. Gate/up (GLU) tiles never split.
-// On MI355X at 65 tokens (W8A16), against one launch over all of K: down_proj 31 us against 82,
-// o_proj 15 against 27, qkv 21 against 28.
+// 129..256, priced at its largest M), N, K and the CU count only, never on M inside the class,
+// so a row's bits do not depend on the batch around it. S is the larger of the count that fills
+// the CUs with 64-row tiles and the count that keeps each range to at most 16 K steps (W8A16) or
+// 48 (W8A8, whose steps cost half as much), capped at 8, at one 256-row block row per CU, at 8
+// K steps per range and at kSplitPartBytes of partials for the class's largest M. Fitted on
+// MI355X by a sweep of S (1..8) and the tile (64, 128, 256 rows) over q/k/v, o_proj and
+// down_proj at 65..256 tokens: summed over those cases, 1.3 % (W8A16) and 0.8 % (W8A8) above the
+// best S per class with the best tile per M, and 8 % below a rule that only fills the CUs with
+// the cost model's tile. Gate/up (GLU) tiles never split.
+constexpr int64_t kSplitPartBytes = 32 << 20;  // the noalloc scratch holds every call's partials
+
 static int tiled_splits(bool i8, int64_t M, int64_t N, int64_t K, int cus) {
   if (M <= LSE_DECODE_MAX_M || M > 256) return 1;
   const int64_t cm = M <= 128 ? 128 : 256;
-  const TiledShape sh = i8 ? tiled_shape<true>(cm, N, cus) : tiled_shape<false>(cm, N, cus);
-  const int64_t tiles = ceil_div(cm, sh.bm) * ceil_div(N, sh.bn);
-  int splits = (int)std::min<int64_t>(8, std::max<int64_t>(1, (cus + tiles / 2) / tiles));
-  while (splits > 1 && ceil_div(K, kTileK) / splits < 8) --splits;
-  return splits;
+  const int64_t nb = ceil_div(N, 128), steps = ceil_div(K, kTileK);
+  int64_t splits = std::max(cus / (ceil_div(cm, 64) * nb), steps / (i8 ? 48 : 16));
+  splits = std::min({splits, (int64_t)8, cus / nb, steps / 8,
+                     kSplitPartBytes / (cm * kTileRows * ceil_div(N, kTileRows) * 4)});
+  return (int)std::max<int64_t>(1, splits);
+}
+
+// The tile of a split launch: the smallest of 64, 128 and 256 rows whose blocks (all splits)
+// fit one round on the CUs, else the cost model's. On MI355X that took down_proj at 129..256
+// tokens (8 splits) from 64 x 128 tiles at two splits, 50-55 us, to one 256 x 128 block row,
+// 39-47 us (W8A16).
+template <bool I8>
+static TiledShape split_tile(int64_t M, int64_t N, int splits, int cus) {
+  const int64_t nb = ceil_div(N, 128);
+  for (int bm : {64, 128, 256})
+    if (ceil_div(M, (int64_t)bm) * nb * splits <= cus) return TiledShape{bm, 128};
+  return tiled_shape<I8>(M, N, cus);
 }
 
 int64_t tiled_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K) {
@@ -583,14 +601,13 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
                                   stream);
   }
   const int cus = device_cus();
-  double cost = 0.0;
-  const TiledShape sh = tiled_shape<I8>(M, N, cus, &cost);
-  const int64_t mblocks = ceil_div(M, sh.bm);
-  const int64_t blocks = mblocks * ceil_div(N, sh.bn);
   const int splits = glu > 0 ? 1 : tiled_splits(I8, M, N, K, cus);
   if (splits > 1) {
     if (!ws || ws_bytes < (int64_t)splits * M * kTileRows * ceil_div(N, kTileRows) * 4)
       return LSE_E_WORKSPACE;
+    const TiledShape sh = split_tile<I8>(M, N, splits, cus);
+    const int64_t mblocks = ceil_div(M, sh.bm);
+    const int64_t blocks = mblocks * ceil_div(N, sh.bn);
     TiledArgs a{};
     a.x = x;
     a.ldx = ldx;
@@ -619,6 +636,10 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
     if (int st = launch_status()) return st;
     return launch_skinny_reduce_parts(I8, ws, s, sx, y, ldy, acc, M, N, splits, stream);
   }
+  double cost = 0.0;
+  const TiledShape sh = tiled_shape<I8>(M, N, cus, &cost);
+  const int64_t mblocks = ceil_div(M, sh.bm);
+  const int64_t blocks = mblocks * ceil_div(N, sh.bn);
   const int64_t full = blocks / cus;  // whole rounds of the chosen tile
   if (!acc && full >= 1 && blocks % cus && (full * cus) % mblocks == 0) {
     const int64_t n_bulk = full * cus / mblocks * sh.bn;

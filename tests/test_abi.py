@@ -55,7 +55,7 @@ def test_query_values(pkg):
     assert _lib.query(_lib.Q_DECODE_MAX_M) == 64
     assert 127 * 127 * _lib.query(_lib.Q_MAX_K) < 2**31
     assert _lib.query(_lib.Q_GFX_ARCH) == 950
-    assert _lib.query(_lib.Q_NOALLOC_SCRATCH) == 16 << 20
+    assert _lib.query(_lib.Q_NOALLOC_SCRATCH) == 32 << 20
     assert _lib.query(99) == -1
 
 

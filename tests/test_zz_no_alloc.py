@@ -44,7 +44,7 @@ def _no_alloc(lib, x, qp, s, m, n, k, stream):
     (14336, 4096, (64, 24)),   # down_proj: the split-K decode route, 8 MiB then 3 MiB of partials
     (4096, 6144, (64, 1)),     # fused qkv: no workspace
     (1024, 272, (300, 40)),    # prefill tile, then a ragged decode shape
-    (14336, 4096, (200, 70)),  # down_proj on the split tiled route, 6.25 MiB then 4.4 MiB
+    (14336, 4096, (200, 70)),  # down_proj on the split tiled route, 25 MiB then 8.75 MiB
 ])
 def test_matches_the_workspace_entry_point(pkg, dev, k, n, ms):
     lib = pkg.library()
@@ -80,7 +80,7 @@ def test_every_llama_decode_shape_fits_the_scratch(pkg):
     """Every Llama-3-8B projection at 1..256 tokens (decode and the split tiled route)."""
     lib = pkg.library()
     cap = lib.lse_query(5)
-    assert cap == 16 << 20
+    assert cap == 32 << 20
     for k, n in [(4096, 6144), (4096, 4096), (4096, 1024), (4096, 28672), (14336, 4096)]:
         for m in range(1, 257):
             assert lib.lse_workspace_bytes(MODE_W8A16, m, n, k) <= cap, (m, k, n)
