@@ -73,7 +73,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true", help="skip prefill and W8A8 figures")
     p.add_argument("--only", choices=["decode", "prefill", "w8a8", "glu", "attention",
-                                      "lm-head", "decode-step", "tp8"],
+                                      "lm-head", "decode-step", "tp8", "mid"],
                    help="one family; decode-step is config 4 (a 32-layer model's decode step)")
     p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
                    help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
@@ -458,6 +458,37 @@ def bench_tp8_shards(pkg, dev, steps: int, gen) -> dict:
                 row[f"M{m}_us"] = round(t * 1e6, 2)
                 row[f"M{m}_gbps"] = round(decode_bytes(m, k, n) / t / 1e9, 1)
         res[f"{name}_{k}x{n}"] = row
+        del copies
+    return res
+
+
+MID_MS = [64, 65, 128, 129, 256]
+
+
+def bench_mid_range(pkg, dev, steps: int, gen) -> dict:
+    """The four Llama-3-8B shapes just above the decode range, where the tiled GEMM splits K for
+    the narrow ones (65..256 tokens; 64 is the decode route, for reference): us per call in
+    W8A16 and in W8A8 (activation quantizer included), each over enough rotated weight copies
+    (at least 768 MB) that every launch streams its weight from HBM, replayed from graphs."""
+    import torch
+
+    res = {"w8a16": {}, "w8a8": {}}
+    for name, (k, n) in zip(SHAPE_NAMES, SHAPES):
+        copies = make_weights(pkg, dev, k, n, -(-768_000_000 // (k * n)), gen)
+        for mode in res:
+            row = {}
+            for m in MID_MS:
+                x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+                if mode == "w8a16":
+                    def step(x=x):
+                        for q, s in copies:
+                            pkg.ops.w8a16_linear(x, q, s)
+                else:
+                    def step(x=x):
+                        for q, s in copies:
+                            pkg.ops.w8a8_linear(x, q, s)
+                row[f"M{m}_us"] = round(time_graph(step, steps) / len(copies) * 1e6, 2)
+            res[mode][name] = row
         del copies
     return res
 
@@ -1308,6 +1339,9 @@ def main() -> None:
     if args.only == "decode-step":
         print(json.dumps({"decode_step": bench_decode_step(pkg, dev, args.steps)}))
         return
+    if args.only == "mid":
+        print(json.dumps({"mid_range": bench_mid_range(pkg, dev, args.steps, gen)}))
+        return
     if args.only == "tp8":
         print(json.dumps({"tp8_shard_shapes": bench_tp8_shards(pkg, dev, args.steps, gen),
                           "device": device_peaks()}))
@@ -1323,6 +1357,7 @@ def main() -> None:
             dev, args.steps, gen, dec["seconds_per_step"])
         secondary["eager_int8_linear"] = bench_eager_overhead(pkg, dev, args.steps, gen)
         secondary["tp8_shard_shapes"] = bench_tp8_shards(pkg, dev, args.steps, gen)
+        secondary["mid_range"] = bench_mid_range(pkg, dev, args.steps, gen)
         secondary["launch_floor"] = bench_launch_floor(pkg, dev, args.steps, gen)
         torch.cuda.empty_cache()
         secondary["decode_step"] = bench_decode_step(pkg, dev, args.steps)
