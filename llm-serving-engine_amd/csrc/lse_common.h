@@ -36,6 +36,11 @@ __device__ __forceinline__ void dequant16(uint4 w, bf16x8& lo, bf16x8& hi) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// XOR swizzle of the 16-byte chunks of a 128-byte bf16 activation row in LDS (64 bf16, one K
+// step): chunk c of row r is stored at c ^ bf16_row_swz(r). Fragment reads of 16 consecutive rows
+// at one chunk offset then hit no LDS bank twice (measured on MI355X with SQ_LDS_BANK_CONFLICT).
+__host__ __device__ constexpr int bf16_row_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
 // D(16x16 fp32) += A(16x32 bf16) · B(32x16 bf16). Lane l supplies A row l%16 and B column
 // l%16, each as 8 values of the 32-long contraction; lanes with equal l/16 supply matching
 // slices. D lands as rows 4*(l/16)+r, r = 0..3, of column l%16.

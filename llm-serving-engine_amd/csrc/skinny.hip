@@ -790,6 +790,19 @@ static bool skinny_deep_tiled(int64_t M, int64_t N, int64_t K) {
   return M > 16 && skinny_split_k(N, K);
 }
 
+int64_t xs_part_bytes(int64_t M, int64_t N, int64_t K);  // xsplit.hip
+int launch_w8a16_xs(const uint16_t* x, int64_t ldx, const int8_t* qp, const float* s,
+                    uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                    int64_t ws_bytes, hipStream_t stream);  // xsplit.hip
+
+// 17..64 tokens over at most 64 row tiles (the k and v projections, tensor-parallel q/k/v
+// shards): the stationary-slice kernel (xsplit.hip), W8A16, when a K range's activations fit its
+// LDS. Chosen by the token class, N and K only.
+static bool skinny_xs(int64_t M, int64_t N, int64_t K) {
+  return M > 16 && ceil_div(N, kTileRows) <= 64 && !skinny_split_k(N, K) &&
+         xs_part_bytes(M, N, K) >= 0;
+}
+
 // The second pass for the tiled kernel's split partial sums (the same [S][M][16 nrb] layout):
 // fp32 partials and y in W8A16, int32 partials, y and acc in W8A8.
 int launch_skinny_reduce_parts(bool i8, const void* part, const float* s, const float* sx,
@@ -817,6 +830,7 @@ int launch_skinny_reduce_parts(bool i8, const void* part, const float* s, const 
 
 int64_t skinny_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K) {
   if (skinny_deep_tiled(M, N, K)) return deep_decode_part_bytes(M, N);
+  if (!i8 && skinny_xs(M, N, K)) return xs_part_bytes(M, N, K);
   return i8 ? skinny_plan<true>(M, N, K).part_bytes : skinny_plan<false>(M, N, K).part_bytes;
 }
 
@@ -847,6 +861,9 @@ static int skinny_run(const void* x, int64_t ldx, const int8_t* qp, const float*
     if (!bfw && glu == 0 && skinny_deep_tiled(M, N, K))
       return launch_w8a16_deep_decode(static_cast<const uint16_t*>(x), ldx, qp, s, y, ldy, M, N,
                                       K, ws, ws_bytes, stream);
+    if (!bfw && glu == 0 && skinny_xs(M, N, K))
+      return launch_w8a16_xs(static_cast<const uint16_t*>(x), ldx, qp, s, y, ldy, M, N, K, ws,
+                             ws_bytes, stream);
   } else {
     const int8_t* xq = static_cast<const int8_t*>(x);
     if (skinny_wide_tiled(M, rows))

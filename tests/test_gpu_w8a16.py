@@ -110,6 +110,17 @@ def test_decode_rejects_a_short_workspace(pkg, dev):
     assert torch.all(y == 0.0)
 
 
+@pytest.mark.parametrize("m", [17, 32, 33, 64])
+@pytest.mark.parametrize("n,k", [(1024, 4096), (768, 4096), (100, 2064), (1000, 4096 + 48)])
+def test_decode_stationary_slice(pkg, dev, m, n, k):
+    """17..64 tokens over at most 64 row tiles (k/v projections, tensor-parallel q/k/v shards):
+    workgroups of four row tiles over one of up to 8 K ranges, the activation slice of the range
+    staged once in LDS, partial sums added in a second pass. (100, 2064): 33 K steps in 7 ranges
+    of 5 with a 3-step last range; (1000, 4144): a ragged last row tile and 65 K steps in 8 ranges
+    of 9, the last ending in a 48-wide K tail."""
+    _check(pkg, dev, m, n, k, 13 * m + n + k, DECODE)
+
+
 @pytest.mark.parametrize(
     "n,k", [(1, 16), (15, 48), (16, 64), (17, 80), (100, 112), (33, 2064), (64, 4096 + 48),
             (16392, 80)]
@@ -172,7 +183,7 @@ def test_output_stride_guard_band(pkg, dev, algo):
 
 
 @pytest.mark.parametrize(
-    "k,n", [(4096, 512), (14336, 4096), (1024, 6144), (8192, 6400), (256, 16400)])
+    "k,n", [(4096, 512), (14336, 4096), (1024, 6144), (8192, 6400), (256, 16400), (4096, 1024)])
 def test_decode_rows_are_batch_invariant(pkg, dev, k, n):
     """A row's result does not depend on M or on the other rows within a token class (M <= 16,
     17..32, 33..64): the graphed decode runs a padded power-of-two bucket while eager decode runs
