@@ -480,22 +480,30 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false) {
 // rounds), per mode, except the 64 x 128 tile's, fitted at M = 256..2048 where it competes. On
 // the Llama-3-8B prefill shapes timed (qkv, o_proj, gate_up, down at M = 256 to 2048, gate_up at
 // 8192) this picks the fastest tile, or one within 6 % (qkv at M = 512).
+// The 64 x 128 tile (four waves) fills the CUs when M is a few hundred and N is narrow, e.g.
+// o_proj and down at M = 256..512: 16-25 % faster than 128 x 128 there, in both modes.
+constexpr int kTileCands = 5;
+constexpr TiledShape kTileCand[kTileCands] = {{256, 256}, {256, 128}, {128, 256}, {128, 128},
+                                              {64, 128}};
+constexpr double kTileEff16[kTileCands] = {1.0, 0.86, 0.87, 0.835, 0.6};
+constexpr double kTileEff8[kTileCands] = {1.0, 0.81, 0.865, 0.86, 0.6};
+
+// One round of candidate i on every CU, in the cost model's units.
+template <bool I8>
+static double tile_round_cost(int i) {
+  return (double)kTileCand[i].bm * kTileCand[i].bn / (I8 ? kTileEff8 : kTileEff16)[i];
+}
+
 template <bool I8>
 static TiledShape tiled_shape(int64_t M, int64_t N, int cus, double* cost_out = nullptr) {
-  // The 64 x 128 tile (four waves) fills the CUs when M is a few hundred and N is narrow, e.g.
-  // o_proj and down at M = 256..512: 16-25 % faster than 128 x 128 there, in both modes.
-  static const TiledShape cand[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 128}};
-  static const double eff16[] = {1.0, 0.86, 0.87, 0.835, 0.6};
-  static const double eff8[] = {1.0, 0.81, 0.865, 0.86, 0.6};
-  const double* eff = I8 ? eff8 : eff16;
-  TiledShape best = cand[0];
+  TiledShape best = kTileCand[0];
   double best_cost = 1e300;
-  for (int i = 0; i < 5; ++i) {
-    const int64_t blocks = ceil_div(M, cand[i].bm) * ceil_div(N, cand[i].bn);
-    const double cost = (double)ceil_div(blocks, (int64_t)cus) * cand[i].bm * cand[i].bn / eff[i];
+  for (int i = 0; i < kTileCands; ++i) {
+    const int64_t blocks = ceil_div(M, kTileCand[i].bm) * ceil_div(N, kTileCand[i].bn);
+    const double cost = (double)ceil_div(blocks, (int64_t)cus) * tile_round_cost<I8>(i);
     if (cost < best_cost * 0.999) {
       best_cost = cost;
-      best = cand[i];
+      best = kTileCand[i];
     }
   }
   if (cost_out) *cost_out = best_cost;
@@ -595,8 +603,8 @@ int64_t tiled_workspace_bytes(bool i8, int64_t M, int64_t N, int64_t K) {
   return splits > 1 ? (int64_t)splits * M * kTileRows * ceil_div(N, kTileRows) * 4 : 0;
 }
 
-// The cost model's tile over all N, except when its tiles leave a partial last round on the CUs
-// (gate_up at M = 2048: 896 tiles of 256 x 256 for 256 CUs, 3.5 rounds) and re-tiling the
+// The cost model's tile over all N, except when a big tile's blocks leave a partial last round on
+// the CUs (gate_up at M = 2048: 896 tiles of 256 x 256 for 256 CUs, 3.5 rounds) and re-tiling the
 // columns of that round fills them better: then the full rounds run as one launch and the
 // remaining columns, with the cost model's tile for them, as a second (gate_up at M = 2048: 768
 // tiles of 256 x 256, then 256 of 128 x 256 over the last 4096 rows). Every output sums its K
@@ -653,23 +661,40 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
   }
   double cost = 0.0;
   const TiledShape sh = tiled_shape<I8>(M, N, cus, &cost);
-  const int64_t mblocks = ceil_div(M, sh.bm);
-  const int64_t blocks = mblocks * ceil_div(N, sh.bn);
-  const int64_t full = blocks / cus;  // whole rounds of the chosen tile
-  if (!acc && full >= 1 && blocks % cus && (full * cus) % mblocks == 0) {
-    const int64_t n_bulk = full * cus / mblocks * sh.bn;
-    if (n_bulk < N) {
-      double tail_cost = 0.0;
-      const TiledShape tsh = tiled_shape<I8>(M, N - n_bulk, cus, &tail_cost);
-      const double bulk_cost = cost * full / (full + 1);  // `full` of the full + 1 rounds
-      if (bulk_cost + tail_cost < 0.97 * cost) {
-        if (int st = launch_tiled_range<I8>(sh, false, x, ldx, qp, s, sx, y, ldy, nullptr, M, N,
-                                            K, glu, 0, n_bulk, stream))
-          return st;
-        return launch_tiled_range<I8>(tsh, false, x, ldx, qp, s, sx, y, ldy, nullptr, M, N, K,
-                                      glu, n_bulk, N - n_bulk, stream);
-      }
+  // Bulk and tail: a 256-row or 256-column tile whose blocks leave a partial last round after
+  // at least one full one runs its full rounds over the first columns, and the cost model's tile
+  // for the rest of N runs as a second launch; taken when some such pair is modelled at least
+  // 3 % under the one launch (the cheapest pair). On MI355X: gate_up at M = 2048 (256 x 256
+  // bulk, 128 x 256 tail) 467 -> 444 us; qkv at M = 4096, in place of 128 x 256 tiles, 198 ->
+  // 184 us (W8A16) and 121 -> 114 us (W8A8). A 128 x 128 bulk with a 64 x 128 tail (qkv at
+  // M = 1024) measured 15 % slower than the model said, so smaller bulk tiles are not tried.
+  double best = 0.97 * cost;
+  int64_t best_bulk = 0;
+  TiledShape bulk_sh{}, tail_sh{};
+  for (int i = 0; i < 3 && !acc; ++i) {
+    const TiledShape c = kTileCand[i];
+    const int64_t mb = ceil_div(M, c.bm);
+    const int64_t blocks = mb * ceil_div(N, c.bn);
+    const int64_t full = blocks / cus;  // whole rounds of candidate i
+    if (full < 1 || blocks % cus == 0 || (full * cus) % mb) continue;
+    const int64_t n_bulk = full * cus / mb * c.bn;
+    if (n_bulk >= N) continue;
+    double tail_cost = 0.0;
+    const TiledShape t = tiled_shape<I8>(M, N - n_bulk, cus, &tail_cost);
+    const double total = full * tile_round_cost<I8>(i) + tail_cost;
+    if (total < best) {
+      best = total;
+      best_bulk = n_bulk;
+      bulk_sh = c;
+      tail_sh = t;
     }
+  }
+  if (best_bulk > 0) {
+    if (int st = launch_tiled_range<I8>(bulk_sh, false, x, ldx, qp, s, sx, y, ldy, nullptr, M,
+                                        N, K, glu, 0, best_bulk, stream))
+      return st;
+    return launch_tiled_range<I8>(tail_sh, false, x, ldx, qp, s, sx, y, ldy, nullptr, M, N, K,
+                                  glu, best_bulk, N - best_bulk, stream);
   }
   return launch_tiled_range<I8>(sh, false, x, ldx, qp, s, sx, y, ldy, acc, M, N, K, glu, 0, N,
                                 stream);

@@ -338,18 +338,21 @@ def test_llama_prefill_shapes_full_size(pkg, dev, k, n):
         assert ok, f"M={m} K={k} N={n}: {msg}"
 
 
-@pytest.mark.parametrize("mode", ["w8a16", "w8a8", "glu"])
-def test_tail_split_launch_changes_no_bit(pkg, dev, mode):
-    """gate_up (K 4096, N 28672) at M = 2048 leaves 3.5 rounds of 256 x 256 tiles on 256 CUs; the
-    tiled GEMM then runs the full rounds and re-tiles the last columns in a second launch. Every
-    output still sums K in increasing order, so the M = 2048 rows equal, bit for bit, the same
-    rows computed at M = 2049, whose 9 block rows do not split."""
-    k, i = 4096, 14336
+@pytest.mark.parametrize("mode,n,m", [
+    ("w8a16", 28672, 2048), ("w8a8", 28672, 2048), ("glu", 28672, 2048),
+    ("w8a16", 6144, 4096), ("w8a8", 6144, 4096)])
+def test_tail_split_launch_changes_no_bit(pkg, dev, mode, n, m):
+    """gate_up (K 4096, N 28672) at M = 2048 leaves 3.5 rounds of 256 x 256 tiles on 256 CUs, and
+    qkv (N 6144) at M = 4096 1.5 rounds; the tiled GEMM then runs the full rounds and re-tiles the
+    last columns (128 x 256) in a second launch. Every output still sums K in increasing order, so
+    the M rows equal, bit for bit, the same rows computed at M + 1, whose block rows do not
+    split."""
+    k = 4096
     gen = torch.Generator(device="cpu").manual_seed(4242)
-    w = (torch.randn(2 * i, k, generator=gen) * 0.02).to(dev)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
     q, s = pkg.ops.quantize_weight_per_channel(w)
     del w
-    x = torch.randn(2049, k, generator=gen).to(torch.bfloat16).to(dev)
+    x = torch.randn(m + 1, k, generator=gen).to(torch.bfloat16).to(dev)
     if mode == "glu":
         qp = pkg.ops.pack_glu(q)
         run = lambda xx: pkg.ops.w8a16_glu(xx, qp, s, algo=PREFILL)  # noqa: E731
@@ -359,5 +362,5 @@ def test_tail_split_launch_changes_no_bit(pkg, dev, mode):
     else:
         qp = pkg.ops.pack_weight(q)
         run = lambda xx: pkg.ops.w8a16_linear(xx, qp, s, algo=PREFILL)  # noqa: E731
-    a, b = run(x[:2048]), run(x)
-    assert torch.equal(a.view(torch.int16), b[:2048].view(torch.int16))
+    a, b = run(x[:m]), run(x)
+    assert torch.equal(a.view(torch.int16), b[:m].view(torch.int16))
