@@ -35,8 +35,9 @@
 //
 // Summation order: the K steps in increasing order, two K=32 MFMAs per step (W8A16) in a fixed
 // chain per output; it depends only on K, or with K splits (65..256 tokens over a narrow weight,
-// tiled_splits) on the split count too: each range's steps in order, then the ranges added in
-// order by a second pass. int32 accumulation (W8A8) is exact in any order.
+// 257..1024 over a deep, narrow one: tiled_splits) on the split count too: each range's steps in
+// order, then the ranges added in order by a second pass. int32 accumulation (W8A8) is exact in
+// any order.
 //
 // Fused gate/up (GLU): with the weight in the gate/up layout (lse_common.h) a block's first row
 // tile is even and a wave's TN row tiles are an even-aligned run, so its tiles j (even, gate) and
@@ -576,8 +577,26 @@ int launch_skinny_reduce_parts(bool i8, const void* part, const float* s, const 
 // the cost model's tile. Gate/up (GLU) tiles never split.
 constexpr int64_t kSplitPartBytes = 32 << 20;  // the noalloc scratch holds every call's partials
 
+// 257..1024 tokens over a deep, narrow weight (at least 128 K steps: the MLP down projection):
+// the cost model's tiles give one block per CU (or fewer), each over all of K, and such a block
+// hides little of its per-step latency. Splitting K fills the CUs with 256 x 128 tiles over S
+// ranges instead: S = 4 at 257..512 tokens (both modes) and S = 2 at 513..1024 (W8A16), fixed
+// per class, taken when the class's largest M gives at most one round of blocks and its partials
+// fit kSplitPartBytes. Measured on MI355X, down_proj (K 14336, N 4096) at M = 512: 94.6 -> 75.1 us
+// (W8A16), 63.6 -> 51.0 us (W8A8); at M = 1024: 143.4 -> 132.4 us (W8A16; W8A8 gained nothing).
+// The shallow projections (K 4096) measured slower with every split and tile tried.
+static int tiled_deep_splits(bool i8, int64_t M, int64_t N, int64_t steps, int cus) {
+  if (steps < 128 || M > (i8 ? 512 : 1024)) return 1;
+  const int64_t cm = M <= 512 ? 512 : 1024;
+  const int64_t splits = cm == 512 ? 4 : 2;
+  if (ceil_div(cm, 256) * ceil_div(N, 128) * splits > cus) return 1;
+  if (splits * cm * kTileRows * ceil_div(N, kTileRows) * 4 > kSplitPartBytes) return 1;
+  return (int)splits;
+}
+
 static int tiled_splits(bool i8, int64_t M, int64_t N, int64_t K, int cus) {
-  if (M <= LSE_DECODE_MAX_M || M > 256) return 1;
+  if (M <= LSE_DECODE_MAX_M) return 1;
+  if (M > 256) return tiled_deep_splits(i8, M, N, ceil_div(K, kTileK), cus);
   const int64_t cm = M <= 128 ? 128 : 256;
   const int64_t nb = ceil_div(N, 128), steps = ceil_div(K, kTileK);
   int64_t splits = std::max(cus / (ceil_div(cm, 64) * nb), steps / (i8 ? 48 : 16));

@@ -107,8 +107,16 @@ def test_workspace_query_and_rejections(pkg):
     for m in (65, 100, 128):
         assert lib.lse_workspace_bytes(0, m, 4096, 14336) * 65 == \
             lib.lse_workspace_bytes(0, 65, 4096, 14336) * m
+    # 257..1024 tokens over a deep, narrow weight: 4 ranges up to 512 tokens, then 2 (W8A16).
+    for m in (257, 400, 512):
+        assert lib.lse_workspace_bytes(0, m, 4096, 14336) == 4 * m * 4096 * 4
+        assert lib.lse_workspace_bytes(1, m, 4096, 14336) == 4 * m * 4096 * 4
+    for m in (513, 1024):
+        assert lib.lse_workspace_bytes(0, m, 4096, 14336) == 2 * m * 4096 * 4
+        assert lib.lse_workspace_bytes(1, m, 4096, 14336) == 0
+    assert lib.lse_workspace_bytes(0, 1025, 4096, 14336) == 0
     for mode in (0, 1):
-        for m in (1, 16, 17, 33, 64, 65, 128, 129, 256):
+        for m in (1, 16, 17, 33, 64, 65, 128, 129, 256, 257, 512, 1024):
             nbytes = lib.lse_workspace_bytes(mode, m, 4096, 14336)
             assert 0 <= nbytes <= 64 * m * (4096 + 15) and nbytes % 16 == 0
     args = (FAKE, 64, FAKE, FAKE, FAKE, 64, 2, 64, 64, 1)

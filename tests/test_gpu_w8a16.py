@@ -209,25 +209,32 @@ def test_decode_rows_are_batch_invariant(pkg, dev, k, n):
 @pytest.mark.parametrize("k,n", [(1024, 256), (14336, 512)])
 def test_prefill_rows_are_batch_invariant(pkg, dev, k, n):
     """The tiled route's token classes (65..128 and 129..256, which may split K over a narrow
-    weight, and > 256): inside a class a row's bits do not depend on M, on the other rows or on
-    zero padding up to the class's power-of-two bucket; across classes rows agree to the
-    tolerance."""
-    x_bits, w = ora.seeded_inputs(32, 400, n, k)
+    weight; 257..512 and 513..1024, which split K over a deep, narrow one; and above): inside a
+    class a row's bits do not depend on M, on the other rows or on zero padding up to the
+    class's largest M; across classes rows agree to the tolerance."""
+    x_bits, w = ora.seeded_inputs(32, 1100, n, k)
     q, s = ora.quantize_weight_per_channel(w)
-    top = {128: _run(pkg, dev, x_bits[:128], q, s, PREFILL),
-           256: _run(pkg, dev, x_bits[:256], q, s, PREFILL),
-           400: _run(pkg, dev, x_bits, q, s, PREFILL)}
+    top = {c: _run(pkg, dev, x_bits[:c], q, s, PREFILL) for c in (128, 256, 512, 1024, 1100)}
     for m, cls in ((65, 128), (100, 128), (127, 128), (129, 256), (200, 256), (255, 256),
-                   (257, 400), (300, 400)):
+                   (257, 512), (300, 512), (511, 512), (513, 1024), (700, 1024), (1025, 1100)):
         np.testing.assert_array_equal(_run(pkg, dev, x_bits[:m], q, s, PREFILL),
                                       top[cls][:m], err_msg=f"M={m}")
-    for m, cls in ((70, 128), (150, 256)):
+    for m, cls in ((70, 128), (150, 256), (400, 512), (600, 1024)):
         padded = x_bits[:cls].copy()
         padded[m:] = 0
         np.testing.assert_array_equal(_run(pkg, dev, padded, q, s, PREFILL)[:m], top[cls][:m])
     golden = ora.w8a16_golden(x_bits[:128], q, s)
-    for cls in (128, 256, 400):
+    for cls in top:
         assert ora.within_tolerance(top[cls][:128], golden)[0]
+
+
+@pytest.mark.parametrize("m", [257, 512, 513, 1024])
+def test_prefill_deep_split_k(pkg, dev, m):
+    """257..1024 tokens over a deep, narrow weight (at least 128 K steps): 4 K ranges at
+    257..512 tokens, 2 at 513..1024, of 256 x 128 tiles, added by the second pass."""
+    nbytes = pkg.library().lse_workspace_bytes(0, m, 512, 14336)
+    assert nbytes == (4 if m <= 512 else 2) * m * 512 * 4
+    _check(pkg, dev, m, 512, 14336, 7 * m + 1, PREFILL)
 
 
 @pytest.mark.parametrize("m", [65, 100, 128, 129, 256])

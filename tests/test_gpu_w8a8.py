@@ -65,6 +65,15 @@ def test_tiled_split_k_bit_exact(pkg, dev, m, n, k):
     _check(pkg, dev, m, n, k, 3 * m + n + k)
 
 
+@pytest.mark.parametrize("m", [257, 512, 513])
+def test_tiled_deep_split_k_bit_exact(pkg, dev, m):
+    """257..512 tokens over a deep, narrow weight: 4 K ranges of 256 x 128 int8 tiles (513 and
+    up: no split in W8A8), bit for bit the oracle's accumulators and outputs."""
+    nbytes = pkg.library().lse_workspace_bytes(1, m, 256, 14336)
+    assert nbytes == (4 * m * 256 * 4 if m <= 512 else 0)
+    _check(pkg, dev, m, 256, 14336, 11 * m + 3)
+
+
 @pytest.mark.parametrize("n,k", [(1, 16), (17, 48), (45, 1072)])
 def test_ragged_shapes_bit_exact(pkg, dev, n, k):
     for m in (1, 40, 90):
