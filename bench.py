@@ -789,8 +789,9 @@ def tiled_calls(trace_dir: str, pmc_dir: str, keep, ms: list[int], k_per_mfma: i
     MFMA busy cycles, engine clocks), each a median over the calls of the sum over the call's
     dispatches. A call is one dispatch, or two when the GEMM re-tiles the columns of a partial
     last round; consecutive dispatches are grouped into calls by their MFMA instruction counts,
-    which sum to the call's (M/16)(N/16)(K/k_per_mfma). `keep` selects the kernel names; every
-    M runs `passes` passes over the four shapes in order."""
+    which sum to the call's (M/16)(N/16)(K/k_per_mfma). A call that splits K is followed by the
+    second pass adding the splits (skinny_reduce); its duration is part of the call's. `keep`
+    selects the kernel names; every M runs `passes` passes over the four shapes in order."""
     import csv
     import statistics
 
@@ -798,8 +799,17 @@ def tiled_calls(trace_dir: str, pmc_dir: str, keep, ms: list[int], k_per_mfma: i
         with open(path, newline="") as f:
             return list(csv.DictReader(f))
 
-    trace = sorted((r for r in read(Path(trace_dir) / "run_kernel_trace.csv")
-                    if keep(r["Kernel_Name"])), key=lambda r: int(r["Start_Timestamp"]))
+    every = sorted((r for r in read(Path(trace_dir) / "run_kernel_trace.csv")
+                    if keep(r["Kernel_Name"]) or "skinny_reduce" in r["Kernel_Name"]),
+                   key=lambda r: int(r["Start_Timestamp"]))
+    trace = [r for r in every if keep(r["Kernel_Name"])]
+    # reduce[j]: the second-pass dispatches between kept dispatch j and the next kept one.
+    reduce: list[list[dict]] = []
+    for r in every:
+        if keep(r["Kernel_Name"]):
+            reduce.append([])
+        elif reduce:
+            reduce[-1].append(r)
     pmc = collections_by_dispatch([r for r in read(Path(pmc_dir) / "run_counter_collection.csv")
                                    if keep(r["Kernel_Name"])], "tiled_gemm_kernel")
     if len(trace) != len(pmc):
@@ -825,9 +835,10 @@ def tiled_calls(trace_dir: str, pmc_dir: str, keep, ms: list[int], k_per_mfma: i
         for si, (k, n) in enumerate(SHAPES):
             cs = calls[(m, si)]
             med = lambda f: statistics.median(sum(f(j) for j in c) for c in cs)  # noqa: E731
-            names = " + ".join(f"`{trace[j]['Kernel_Name'].split('(')[0].replace('void lse::', '')}`"
-                               for j in cs[0])
-            rows.append((m, SHAPE_NAMES[si], k, n, names, med(lambda j: dur(trace[j])),
+            short = lambda r: f"`{r['Kernel_Name'].split('(')[0].replace('void lse::', '')}`"  # noqa: E731
+            names = " + ".join(short(r) for j in cs[0] for r in [trace[j], *reduce[j]])
+            rows.append((m, SHAPE_NAMES[si], k, n, names,
+                         med(lambda j: dur(trace[j]) + sum(dur(r) for r in reduce[j])),
                          med(lambda j: pmc[j]["SQ_INSTS_MFMA"]),
                          med(lambda j: pmc[j]["SQ_VALU_MFMA_BUSY_CYCLES"]),
                          med(lambda j: pmc[j]["GRBM_GUI_ACTIVE"]) / XCDS))
