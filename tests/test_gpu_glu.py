@@ -128,7 +128,7 @@ def test_w8a8_within_one_ulp(pkg, dev, m, i, k):
 
 
 def test_w8a8_llama_gate_up_full_size(pkg, dev):
-    for m in (1, 64, 512):
+    for m in (1, 64, 100, 512):
         _check_w8a8(pkg, dev, m, 14336, 4096, 50 + m)
 
 
