@@ -104,10 +104,12 @@ tiled_gemm_kernel(TiledArgs a) {
   constexpr int WTILES = BN / 16;           // weight tiles per stage
   constexpr int WH = BFW ? 2 : 1;           // 1 KB pieces per weight tile and stage
   constexpr int XI = XBYTES / (W * 1024);   // direct-to-LDS loads per wave per stage, x
-  constexpr int WI = WTILES * WH / W;       // ... weights
+  // ... weights: WTILES WH pieces of 1 KB over W waves; when W does not divide them (192-row
+  // tiles: 12 over 8) the last loads fall past the tiles, read zeros into padding and move no data.
+  constexpr int WI = (WTILES * WH + W - 1) / W;
   constexpr int LOADS = XI + WI;
   static_assert(TM >= 1 && TN >= 1, "wave grid must tile the block");
-  static_assert(XBYTES % (W * 1024) == 0 && (WTILES * WH) % W == 0, "whole 1 KB loads per wave");
+  static_assert(XBYTES % (W * 1024) == 0, "whole 1 KB x loads per wave");
   static_assert(NST >= 3 && NST <= 4, "three or four stage slots");
   static_assert((NST - 2) * LOADS < 64, "vmcnt holds at most 63");
   static_assert(!GLU || TN % 2 == 0, "gate/up wave tiles hold whole pairs of row tiles");
@@ -117,8 +119,8 @@ tiled_gemm_kernel(TiledArgs a) {
   // rows (2 x 4) it measured 3-5 % slower, so those keep the plain schedule.
   constexpr bool WAHEAD = !I8 && !BFW && WGM == 1;
 
-  // One LDS array per stage slot (x image, then the weight tiles).
-  constexpr int SLOT = (XBYTES + WTILES * WH * 1024) / 16;
+  // One LDS array per stage slot (x image, then the weight tiles and their padding).
+  constexpr int SLOT = (XBYTES + WI * W * 1024) / 16;
   __shared__ uint4 st0[SLOT], st1[SLOT], st2[SLOT], st3[NST > 3 ? SLOT : 1];
   auto xslot = [&](int i) -> uint4* {
     switch (i) {
@@ -478,6 +480,10 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
       return reinterpret_cast<const void*>(&tiled_gemm_kernel<true, 64, 128, 2, 2, 4, GLU>);
   }
   if (sh.bm == 256 && sh.bn == 256) return tiled_fn<I8, 256, 256, GLU>();
+  if (sh.bm == 256 && sh.bn == 192) {
+    if constexpr (GLU) return nullptr;  // never chosen for gate/up (tiled_shape)
+    else return tiled_fn<I8, 256, 192, false>();
+  }
   if (sh.bm == 256 && sh.bn == 128) return tiled_fn<I8, 256, 128, GLU>();
   if (sh.bm == 128 && sh.bn == 256) return tiled_fn<I8, 128, 256, GLU>();
   if (one_row)
@@ -495,11 +501,15 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
 // 8192) this picks the fastest tile, or one within 6 % (qkv at M = 512).
 // The 64 x 128 tile (four waves) fills the CUs when M is a few hundred and N is narrow, e.g.
 // o_proj and down at M = 256..512: 16-25 % faster than 128 x 128 there, in both modes.
-constexpr int kTileCands = 5;
+// The 256 x 192 tile (2 x 4 waves of 128 x 48) gives 6144-row weights (the fused q/k/v) one
+// round of 256 blocks at M = 2048: on MI355X W8A16 97.6 us there against 103-114 us for the
+// 128 x 128 tiles (W8A8 on par), 0.92-0.93 of the 256 x 256 tile's rate at M = 8192. Gate/up
+// tiles hold whole pairs of row tiles, so it is not a candidate for them.
+constexpr int kTileCands = 6;
 constexpr TiledShape kTileCand[kTileCands] = {{256, 256}, {256, 128}, {128, 256}, {128, 128},
-                                              {64, 128}};
-constexpr double kTileEff16[kTileCands] = {1.0, 0.86, 0.87, 0.835, 0.6};
-constexpr double kTileEff8[kTileCands] = {1.0, 0.81, 0.865, 0.86, 0.6};
+                                              {64, 128},  {256, 192}};
+constexpr double kTileEff16[kTileCands] = {1.0, 0.86, 0.87, 0.835, 0.6, 0.92};
+constexpr double kTileEff8[kTileCands] = {1.0, 0.81, 0.865, 0.86, 0.6, 0.926};
 
 // One round of candidate i on every CU, in the cost model's units.
 template <bool I8>
@@ -508,10 +518,12 @@ static double tile_round_cost(int i) {
 }
 
 template <bool I8>
-static TiledShape tiled_shape(int64_t M, int64_t N, int cus, double* cost_out = nullptr) {
+static TiledShape tiled_shape(int64_t M, int64_t N, int cus, double* cost_out = nullptr,
+                              bool glu = false) {
   TiledShape best = kTileCand[0];
   double best_cost = 1e300;
   for (int i = 0; i < kTileCands; ++i) {
+    if (glu && kTileCand[i].bn == 192) continue;  // 2 x 4 waves of 3 row tiles: not pairs
     const int64_t blocks = ceil_div(M, kTileCand[i].bm) * ceil_div(N, kTileCand[i].bn);
     const double cost = (double)ceil_div(blocks, (int64_t)cus) * tile_round_cost<I8>(i);
     if (cost < best_cost * 0.999) {
@@ -566,6 +578,7 @@ static int launch_tiled_range(const TiledShape& sh, bool decode, const void* x, 
   const bool one_row = a.mblocks == 1;
   const void* fn = glu > 0 ? tiled_kernel_for<I8, true>(sh, decode, one_row)
                             : tiled_kernel_for<I8, false>(sh, decode, one_row);
+  if (!fn) return LSE_E_RANGE;
   const hipError_t e =
       hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(threads), args, 0, stream);
   return e == hipSuccess ? launch_status() : (int)e;
@@ -692,7 +705,7 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
     return launch_skinny_reduce_parts(I8, ws, s, sx, y, ldy, acc, M, N, splits, stream);
   }
   double cost = 0.0;
-  const TiledShape sh = tiled_shape<I8>(M, N, cus, &cost);
+  const TiledShape sh = tiled_shape<I8>(M, N, cus, &cost, glu > 0);
   // Bulk and tail: a 256-row or 256-column tile whose blocks leave a partial last round after
   // at least one full one runs its full rounds over the first columns, and the cost model's tile
   // for the rest of N runs as a second launch; taken when some such pair is modelled at least
@@ -712,7 +725,7 @@ static int launch_tiled(const void* x, int64_t ldx, const int8_t* qp, const floa
     const int64_t n_bulk = full * cus / mb * c.bn;
     if (n_bulk >= N) continue;
     double tail_cost = 0.0;
-    const TiledShape t = tiled_shape<I8>(M, N - n_bulk, cus, &tail_cost);
+    const TiledShape t = tiled_shape<I8>(M, N - n_bulk, cus, &tail_cost, glu > 0);
     const double total = full * tile_round_cost<I8>(i) + tail_cost;
     if (total < best) {
       best = total;

@@ -345,6 +345,29 @@ def test_llama_prefill_shapes_full_size(pkg, dev, k, n):
         assert ok, f"M={m} K={k} N={n}: {msg}"
 
 
+@pytest.mark.parametrize("m,n", [(1500, 6000), (2048, 6144)])
+def test_prefill_192_row_tiles(pkg, dev, m, n):
+    """6000 and 6144 rows at 1500 and 2048 tokens: on 256 CUs the tile model picks 256 x 192
+    tiles (one round of 192 or 256 blocks; 6000 ends in a block of 3 of its 12 row tiles), whose
+    eight waves take 12 weight tiles in two loads each, the last four past the tiles. Against the
+    fp64 product on the GPU, and row for row the same bits as the first 1100 rows run alone
+    (128 x 128 tiles): every tile sums K in increasing order."""
+    k = 4096
+    gen = torch.Generator(device="cpu").manual_seed(1920 + m + n)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
+    q, s = pkg.ops.quantize_weight_per_channel(w)
+    del w
+    qp = pkg.ops.pack_weight(q)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+    y = pkg.ops.w8a16_linear(x, qp, s, algo=PREFILL)
+    golden = (x.double() @ q.double().t()) * s.double()[None, :]
+    ok, msg = check_rows_in_chunks(y, golden)
+    assert ok, f"M={m} N={n}: {msg}"
+    del golden
+    y_small = pkg.ops.w8a16_linear(x[:1100], qp, s, algo=PREFILL)
+    assert torch.equal(y[:1100].view(torch.int16), y_small.view(torch.int16))
+
+
 @pytest.mark.parametrize("mode,n,m", [
     ("w8a16", 28672, 2048), ("w8a8", 28672, 2048), ("glu", 28672, 2048),
     ("w8a16", 6144, 4096), ("w8a8", 6144, 4096)])

@@ -141,6 +141,25 @@ def test_llama_shapes_at_4096_tokens(pkg, dev, k, n):
         np.testing.assert_array_equal(bf16_bits(y[r0:r0 + 1024]), y_ref, err_msg=f"rows {r0}..")
 
 
+@pytest.mark.parametrize("m,n", [(1500, 6000), (2048, 6144)])
+def test_tiled_192_row_tiles_bit_exact(pkg, dev, m, n):
+    """The 256 x 192 tile the model picks for 6000 and 6144 rows at 1500 and 2048 tokens (on 256
+    CUs), with a last block of 3 row tiles for 6000: accumulators exactly against an fp64 GEMM on
+    the GPU, outputs against the oracle's epilogue."""
+    k = 4096
+    x_bits, w = ora.seeded_inputs(1930 + m + n, m, n, k, outliers=True)
+    q, s = pkg.ops.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    del w
+    qp = pkg.ops.pack_weight(q)
+    xq, sx = pkg.ops.quantize_act_per_token(to_bf16_tensor(x_bits, dev))
+    y, acc = pkg.ops.w8a8_gemm(xq, sx, qp, s, True)
+    exact = (xq.double() @ q.double().t()).round().to(torch.int64)
+    assert torch.equal(acc.to(torch.int64), exact), f"M={m} N={n}"
+    del exact
+    y_ref = ora.w8a8_epilogue(acc.cpu().numpy(), sx.cpu().numpy(), s.cpu().numpy())
+    np.testing.assert_array_equal(bf16_bits(y), y_ref)
+
+
 def test_acc_only_and_y_only(pkg, dev):
     x_bits, w = ora.seeded_inputs(61, 20, 64, 256, outliers=True)
     q, s = ora.quantize_weight_per_channel(w)
