@@ -263,6 +263,21 @@ int persistent_blocks(const void* kernel, int threads, size_t dyn_lds = 0);
 // gets 1), q = clamp(rne(fl32(v / scale)), -127, 127).
 __device__ __forceinline__ float row_scale(float amax) { return amax > 0.0f ? amax / 127.0f : 1.0f; }
 
+// The same quantization of a bf16 value v from the row's reciprocal inv = fl32(1 / scale), for
+// scales of at least kQuantRecipMinScale: q0 = fl32(v inv) is within an ulp of v / scale, the
+// residual fma(-q0, scale, v) is exact, and fma(residual, inv, q0) is fl32(v / scale) (the
+// quotient correction with a correctly rounded reciprocal of P. Markstein, IBM J. Res. Dev.
+// 34(1), 1990). Three operations instead of a correctly rounded division per element. Checked
+// exhaustively (tests/quant_recip_check.c): for every bf16 amax whose scale is in range and every
+// bf16 v with |v| <= amax it gives quant1's result (q0 alone differs in 5304 of those 5.2e8).
+constexpr float kQuantRecipMinScale = 0x1p-100f;
+
+__device__ __forceinline__ int8_t quant1_recip(float v, float scale, float inv) {
+  const float q0 = v * inv;
+  const float t = __builtin_rintf(__builtin_fmaf(__builtin_fmaf(-q0, scale, v), inv, q0));
+  return (int8_t)fminf(fmaxf(t, -127.0f), 127.0f);
+}
+
 __device__ __forceinline__ int8_t quant1(float v, float scale) {
   const float t = __builtin_rintf(v / scale);
   return (int8_t)fminf(fmaxf(t, -127.0f), 127.0f);

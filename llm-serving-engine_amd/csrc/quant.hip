@@ -23,6 +23,32 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 
+// Eight bf16 values (four packed pairs, low half first) quantized by `q` into eight int8 bytes.
+template <typename Q>
+__device__ __forceinline__ uint2 quant8(const uint32_t (&u)[4], Q q) {
+  uint32_t packed[2] = {0, 0};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = (uint8_t)q(__builtin_bit_cast(float, u[j] << 16));
+    const uint32_t hi = (uint8_t)q(__builtin_bit_cast(float, u[j] & 0xffff0000u));
+    packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
+  }
+  return make_uint2(packed[0], packed[1]);
+}
+
+// Runs `body(q)` with the row's element quantizer: from the reciprocal of the scale where that
+// gives quant1's results (scale >= kQuantRecipMinScale, every bf16 row but the tiniest), else by
+// division. The branch is uniform over the workgroup (one row).
+template <typename F>
+__device__ __forceinline__ void with_row_quantizer(float scale, F body) {
+  if (scale >= kQuantRecipMinScale) {
+    const float inv = 1.0f / scale;
+    body([=](float v) { return quant1_recip(v, scale, inv); });
+  } else {
+    body([=](float v) { return quant1(v, scale); });
+  }
+}
+
 // One workgroup per weight row; fp32 input read twice (the second pass hits L2).
 __global__ void __launch_bounds__(kQuantThreads)
 quantize_weight_rows(const float* __restrict__ w, int64_t ldw, int8_t* __restrict__ q,
@@ -48,7 +74,7 @@ quantize_weight_rows(const float* __restrict__ w, int64_t ldw, int8_t* __restric
   }
 }
 
-// One workgroup per token; bf16 input read twice (the second pass hits L2). Rows longer than 8192
+// One workgroup per token; bf16 input read twice (the second pass hits L2). Rows longer than 16384
 // elements; shorter ones take quantize_act_rows_reg.
 __global__ void __launch_bounds__(kQuantThreads)
 quantize_act_rows(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ xq,
@@ -69,18 +95,13 @@ quantize_act_rows(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restric
   const float scale = row_scale(block_max(amax, red));
   if (threadIdx.x == 0) sx[m] = scale;
   int8_t* out = xq + m * K;
-  for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
-    const uint4 v = *reinterpret_cast<const uint4*>(row + k);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t packed[2] = {0, 0};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, w[i] << 16), scale);
-      const uint32_t hi = (uint8_t)quant1(__builtin_bit_cast(float, w[i] & 0xffff0000u), scale);
-      packed[i >> 1] |= (lo | (hi << 8)) << (16 * (i & 1));
+  with_row_quantizer(scale, [&](auto q) {
+    for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(row + k);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      *reinterpret_cast<uint2*>(out + k) = quant8(w, q);
     }
-    *reinterpret_cast<uint2*>(out + k) = make_uint2(packed[0], packed[1]);
-  }
+  });
 }
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -103,7 +124,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 //   r = 1 / sqrt(fl32(sum_k x^2 / K) + eps),  h_k = bf16(w_k * bf16(x_k * r))
 // then sx = fl32(amax_k |h_k| / 127) and xq_k = clamp(rne(h_k / sx), -127, 127), exactly as
 // quantize_act_rows does for an existing bf16 row. One workgroup per token; the row is read three
-// times (sum of squares, amax, quantize), the last two from L2 (rows longer than 8192 elements;
+// times (sum of squares, amax, quantize), the last two from L2 (rows longer than 16384 elements;
 // shorter ones take rmsnorm_quant_rows_reg). `normed` (optional) receives h.
 __device__ __forceinline__ float rms_h(uint32_t xb, uint32_t wb, float r) {
   const float x = __builtin_bit_cast(float, xb);
@@ -151,23 +172,22 @@ rmsnorm_quant_rows(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* 
   const float scale = row_scale(block_max(amax, red));
   if (threadIdx.x == 0) sx[m] = scale;
   int8_t* out = xq + m * K;
-  for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
-    const uint4 v = *reinterpret_cast<const uint4*>(row + k);
-    const uint4 g = *reinterpret_cast<const uint4*>(w + k);
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w}, gw[4] = {g.x, g.y, g.z, g.w};
-    uint32_t packed[2] = {0, 0};
+  with_row_quantizer(scale, [&](auto q) {
+    for (int k = threadIdx.x * 8; k < K; k += kQuantThreads * 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(row + k);
+      const uint4 g = *reinterpret_cast<const uint4*>(w + k);
+      const uint32_t u[4] = {v.x, v.y, v.z, v.w}, gw[4] = {g.x, g.y, g.z, g.w};
+      uint32_t hb[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = (uint8_t)quant1(rms_h(u[i] << 16, gw[i] << 16, r), scale);
-      const uint32_t hi =
-          (uint8_t)quant1(rms_h(u[i] & 0xffff0000u, gw[i] & 0xffff0000u, r), scale);
-      packed[i >> 1] |= (lo | (hi << 8)) << (16 * (i & 1));
+      for (int i = 0; i < 4; ++i)
+        hb[i] = pack_bf16x2(rms_h(u[i] << 16, gw[i] << 16, r),
+                            rms_h(u[i] & 0xffff0000u, gw[i] & 0xffff0000u, r));
+      *reinterpret_cast<uint2*>(out + k) = quant8(hb, q);
     }
-    *reinterpret_cast<uint2*>(out + k) = make_uint2(packed[0], packed[1]);
-  }
+  });
 }
 
-// The same for rows of at most NV x 2048 elements (hidden sizes up to 8192): thread t keeps
+// The same for rows of at most NV x 2048 elements (hidden sizes up to 16384): thread t keeps
 // elements 8 t + 2048 i (i < NV) of x and of the weight in registers, so the row is read once and
 // the normed row is quantized from registers. Slots past K hold zeros, which add exact zeros to
 // the sum of squares and to nothing else; the arithmetic and every order of summation are those
@@ -218,19 +238,13 @@ rmsnorm_quant_rows_reg(const uint16_t* __restrict__ x, int64_t ldx, const uint16
   const float scale = row_scale(block_max(amax, red));
   if (threadIdx.x == 0) sx[m] = scale;
   int8_t* out = xq + m * K;
+  with_row_quantizer(scale, [&](auto q) {
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
-    if (k >= K) continue;
-    uint32_t packed[2] = {0, 0};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, hb[i][j] << 16), scale);
-      const uint32_t hi = (uint8_t)quant1(__builtin_bit_cast(float, hb[i][j] & 0xffff0000u), scale);
-      packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
+    for (int i = 0; i < NV; ++i) {
+      const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
+      if (k < K) *reinterpret_cast<uint2*>(out + k) = quant8(hb[i], q);
     }
-    *reinterpret_cast<uint2*>(out + k) = make_uint2(packed[0], packed[1]);
-  }
+  });
 }
 
 int launch_rmsnorm_quantize(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
@@ -246,6 +260,9 @@ int launch_rmsnorm_quantize(const uint16_t* x, int64_t ldx, const uint16_t* w, f
                        normed, (int)K);
   else if (K <= 4 * kRow)
     hipLaunchKernelGGL(rmsnorm_quant_rows_reg<4>, grid, block, 0, stream, x, ldx, w, eps, xq, sx,
+                       normed, (int)K);
+  else if (K <= 8 * kRow)
+    hipLaunchKernelGGL(rmsnorm_quant_rows_reg<8>, grid, block, 0, stream, x, ldx, w, eps, xq, sx,
                        normed, (int)K);
   else
     hipLaunchKernelGGL(rmsnorm_quant_rows, grid, block, 0, stream, x, ldx, w, eps, xq, sx, normed,
@@ -286,19 +303,13 @@ quantize_act_rows_reg(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __res
   const float scale = row_scale(block_max(amax, red));
   if (threadIdx.x == 0) sx[m] = scale;
   int8_t* out = xq + m * K;
+  with_row_quantizer(scale, [&](auto q) {
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
-    if (k >= K) continue;
-    uint32_t packed[2] = {0, 0};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, u[i][j] << 16), scale);
-      const uint32_t hi = (uint8_t)quant1(__builtin_bit_cast(float, u[i][j] & 0xffff0000u), scale);
-      packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
+    for (int i = 0; i < NV; ++i) {
+      const int k = threadIdx.x * 8 + kQuantThreads * 8 * i;
+      if (k < K) *reinterpret_cast<uint2*>(out + k) = quant8(u[i], q);
     }
-    *reinterpret_cast<uint2*>(out + k) = make_uint2(packed[0], packed[1]);
-  }
+  });
 }
 
 int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, int64_t M,
@@ -311,6 +322,8 @@ int launch_quantize_act(const uint16_t* x, int64_t ldx, int8_t* xq, float* sx, i
     hipLaunchKernelGGL(quantize_act_rows_reg<2>, grid, block, 0, stream, x, ldx, xq, sx, (int)K);
   else if (K <= 4 * kRow)
     hipLaunchKernelGGL(quantize_act_rows_reg<4>, grid, block, 0, stream, x, ldx, xq, sx, (int)K);
+  else if (K <= 8 * kRow)
+    hipLaunchKernelGGL(quantize_act_rows_reg<8>, grid, block, 0, stream, x, ldx, xq, sx, (int)K);
   else
     hipLaunchKernelGGL(quantize_act_rows, grid, block, 0, stream, x, ldx, xq, sx, (int)K);
   return launch_status();
