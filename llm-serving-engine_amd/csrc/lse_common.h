@@ -283,6 +283,19 @@ __device__ __forceinline__ int8_t quant1(float v, float scale) {
   return (int8_t)fminf(fmaxf(t, -127.0f), 127.0f);
 }
 
+// Runs `body(q)` with a row's element quantizer q(v) (bf16 v): from the reciprocal of the scale
+// where that gives quant1's results (scale >= kQuantRecipMinScale, every bf16 row but the
+// tiniest), else by division.
+template <typename F>
+__device__ __forceinline__ void with_row_quantizer(float scale, F body) {
+  if (scale >= kQuantRecipMinScale) {
+    const float inv = 1.0f / scale;
+    body([=](float v) { return quant1_recip(v, scale, inv); });
+  } else {
+    body([=](float v) { return quant1(v, scale); });
+  }
+}
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LSE_OK : (int)e;

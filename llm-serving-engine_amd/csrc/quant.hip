@@ -36,19 +36,6 @@ __device__ __forceinline__ uint2 quant8(const uint32_t (&u)[4], Q q) {
   return make_uint2(packed[0], packed[1]);
 }
 
-// Runs `body(q)` with the row's element quantizer: from the reciprocal of the scale where that
-// gives quant1's results (scale >= kQuantRecipMinScale, every bf16 row but the tiniest), else by
-// division. The branch is uniform over the workgroup (one row).
-template <typename F>
-__device__ __forceinline__ void with_row_quantizer(float scale, F body) {
-  if (scale >= kQuantRecipMinScale) {
-    const float inv = 1.0f / scale;
-    body([=](float v) { return quant1_recip(v, scale, inv); });
-  } else {
-    body([=](float v) { return quant1(v, scale); });
-  }
-}
-
 // One workgroup per weight row; fp32 input read twice (the second pass hits L2).
 __global__ void __launch_bounds__(kQuantThreads)
 quantize_weight_rows(const float* __restrict__ w, int64_t ldw, int8_t* __restrict__ q,

@@ -228,8 +228,8 @@ skinny_kernel(SkinnyArgs a) {
     if constexpr (QX) {
       // Per-token quantization of the bf16 rows into the staged int8 image, bit for bit what
       // quantize_act_rows computes: each row's max |x| (an LDS atomic max on the float bits,
-      // which order like the values since they are >= 0), then every element's quant1 with the
-      // row's scale, written at its swizzled position (chunk pc of row m holds logical chunk
+      // which order like the values since they are >= 0), then every element quantized with the
+      // row's scale (with_row_quantizer: quant1's results), written at its swizzled position (chunk pc of row m holds logical chunk
       // pc ^ (m & xswz); K is a multiple of 16, so a 16-element chunk is wholly in or out).
       // Work item c is physical chunk c of the staged image (16 int8 of row c / rch), i.e. 16
       // bf16 of x (logical chunk pc ^ (m & xswz), zeros past K). A thread keeps its first QR
@@ -263,15 +263,17 @@ skinny_kernel(SkinnyArgs a) {
       auto quant_item = [&](int c, const uint4& v0, const uint4& v1) {
         const float scale = row_scale(__builtin_bit_cast(float, qx_amax[c / rch]));
         const uint32_t w8[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        uint32_t packed[4] = {0, 0, 0, 0};
+        with_row_quantizer(scale, [&](auto q) {
+          uint32_t packed[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint32_t lo = (uint8_t)quant1(__builtin_bit_cast(float, w8[j] << 16), scale);
-          const uint32_t hi = (uint8_t)quant1(__builtin_bit_cast(float, w8[j] & 0xffff0000u), scale);
-          packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
-        }
-        *reinterpret_cast<uint4*>(x_lds + 16 * c) =
-            make_uint4(packed[0], packed[1], packed[2], packed[3]);
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t lo = (uint8_t)q(__builtin_bit_cast(float, w8[j] << 16));
+            const uint32_t hi = (uint8_t)q(__builtin_bit_cast(float, w8[j] & 0xffff0000u));
+            packed[j >> 1] |= (lo | (hi << 8)) << (16 * (j & 1));
+          }
+          *reinterpret_cast<uint4*>(x_lds + 16 * c) =
+              make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        });
       };
       constexpr int QR = 2;
       uint4 kv0[QR], kv1[QR];
