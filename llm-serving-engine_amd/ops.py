@@ -275,24 +275,26 @@ def w8a8_gemm(
     return y, acc
 
 
-ONE_LAUNCH_W8A8_MAX_ROWS = 2  # rows up to which w8a8_linear takes the one-launch kernel
+# Elements of x (M * K) up to which w8a8_linear takes the one-launch kernel.
+ONE_LAUNCH_W8A8_MAX_ELEMS = 14336
 
 
 def w8a8_linear(x: torch.Tensor, qp: torch.Tensor, scales: torch.Tensor,
                 want_acc: bool = False, one_launch: bool | None = None):
     """Dynamic per-token W8A8: quantize x per row, int8 GEMM with exact int32 accumulation,
     y = bf16((acc * sx[m]) * s[n]). x (..., K) bf16 → y (..., N) bf16 (with want_acc, also the
-    (M, N) int32 accumulators). One or two rows run as one kernel that quantizes while it
-    stages x (`lse_w8a8_linear`); more rows quantize first, then run the GEMM. Both give the same
-    bits. The one-launch kernel quantizes all of x in every workgroup, which from 4 rows up costs
-    more than the second launch saves (measured on MI355X over the Llama-3-8B shapes: 6-17 %
-    faster at 1 row, mostly faster at 2, 5-80 % slower from 4 to 16). `one_launch` True takes
-    the one-launch kernel wherever it runs (`lse_w8a8_linear_supported`), False never."""
+    (M, N) int32 accumulators). Up to ONE_LAUNCH_W8A8_MAX_ELEMS elements of x (1 to 3 rows of
+    4096, 1 row of 14336) run as one kernel that quantizes while it stages x (`lse_w8a8_linear`);
+    more quantize first, then run the GEMM. Both give the same bits. The one-launch kernel
+    quantizes all of x in every workgroup, so its cost grows with M * K: measured on MI355X over
+    the Llama-3-8B shapes it is 3-16 % faster up to 14336 elements, and 6 % slower at 2 x 14336
+    (down_proj) and up to 6 % at 4 x 4096. `one_launch` True takes the one-launch kernel wherever
+    it runs (`lse_w8a8_linear_supported`), False never."""
     n, k = scales.shape[0], x.shape[-1]
     lib = _lib.library()
     m = x.numel() // k if k else 0
     if one_launch is None:
-        one_launch = m <= ONE_LAUNCH_W8A8_MAX_ROWS
+        one_launch = m * k <= ONE_LAUNCH_W8A8_MAX_ELEMS
     if m and one_launch and lib.lse_w8a8_linear_supported(m, k):
         dev = _on_gpu(x, qp, scales)
         _require(x.dtype == torch.bfloat16, f"W8A8 expects bf16 activations, got {x.dtype}")
