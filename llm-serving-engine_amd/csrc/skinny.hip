@@ -666,8 +666,14 @@ static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K, bool glu = fals
   const int rt = std::max(skinny_rt(N), glu ? 2 : 1);
   // 17..32 tokens over single-row-tile panels (o_proj, k/v): one wave per SIMD with 4-deep
   // activation rings keeps more activation bytes in flight than two waves with 2-deep ones; on
-  // MI355X in W8A16 7-10 % faster (o_proj 8.4 against 9.2 us at 32 tokens).
-  if (mt == 2) return {2, rt, rt == 4 || (rt == 1 && !I8) ? 4 : 8, 4, false, 1};
+  // MI355X in W8A16 7-10 % faster (o_proj 8.4 against 9.2 us at 32 tokens). W8A8 likewise above
+  // 64 row tiles (o_proj 7.20 against 7.79 us at 32 tokens, the tensor-parallel o_proj and
+  // down_proj shards 6-12 %); k/v (64 row tiles, 64 workgroups) keeps eight waves (3-7 % faster
+  // at 17 tokens).
+  if (mt == 2) {
+    const bool four = rt == 4 || (rt == 1 && (!I8 || ceil_div(N, kTileRows) > 64));
+    return {2, rt, four ? 4 : 8, 4, false, 1};
+  }
   // 64 tokens: two waves per SIMD (eight per workgroup); a weight ring of 4 for single row
   // tiles (o_proj: 5 % faster than one wave per SIMD), 2 for 32- and 64-row panels.
   return rt == 1 ? SkinnyShape{4, 1, 8, 4, false, 1} : SkinnyShape{4, rt, 8, 2, false, 1};
