@@ -481,8 +481,8 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
   }
   if (sh.bm == 256 && sh.bn == 256) return tiled_fn<I8, 256, 256, GLU>();
   if (sh.bm == 256 && sh.bn == 192) {
-    if constexpr (GLU) return nullptr;  // never chosen for gate/up (tiled_shape)
-    else return tiled_fn<I8, 256, 192, false>();
+    if constexpr (I8 || GLU) return nullptr;  // W8A16 without gate/up only (tiled_shape)
+    else return tiled_fn<false, 256, 192, false>();
   }
   if (sh.bm == 256 && sh.bn == 128) return tiled_fn<I8, 256, 128, GLU>();
   if (sh.bm == 128 && sh.bn == 256) return tiled_fn<I8, 128, 256, GLU>();
@@ -503,13 +503,13 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
 // o_proj and down at M = 256..512: 16-25 % faster than 128 x 128 there, in both modes.
 // The 256 x 192 tile (2 x 4 waves of 128 x 48) gives 6144-row weights (the fused q/k/v) one
 // round of 256 blocks at M = 2048: on MI355X W8A16 97.6 us there against 103-114 us for the
-// 128 x 128 tiles (W8A8 on par), 0.92-0.93 of the 256 x 256 tile's rate at M = 8192. Gate/up
-// tiles hold whole pairs of row tiles, so it is not a candidate for them.
+// 128 x 128 tiles, 0.92 of the 256 x 256 tile's rate at M = 8192. Only W8A16 non-gate/up
+// launches consider it (tiled_shape).
 constexpr int kTileCands = 6;
 constexpr TiledShape kTileCand[kTileCands] = {{256, 256}, {256, 128}, {128, 256}, {128, 128},
                                               {64, 128},  {256, 192}};
 constexpr double kTileEff16[kTileCands] = {1.0, 0.86, 0.87, 0.835, 0.6, 0.92};
-constexpr double kTileEff8[kTileCands] = {1.0, 0.81, 0.865, 0.86, 0.6, 0.926};
+constexpr double kTileEff8[kTileCands] = {1.0, 0.81, 0.865, 0.86, 0.6, 0.926};  // 256 x 192 unused
 
 // One round of candidate i on every CU, in the cost model's units.
 template <bool I8>
@@ -523,7 +523,9 @@ static TiledShape tiled_shape(int64_t M, int64_t N, int cus, double* cost_out = 
   TiledShape best = kTileCand[0];
   double best_cost = 1e300;
   for (int i = 0; i < kTileCands; ++i) {
-    if (glu && kTileCand[i].bn == 192) continue;  // 2 x 4 waves of 3 row tiles: not pairs
+    // 256 x 192: W8A16 only (in W8A8 on par at M = 2048, 3-9 % slower than the bulk-and-tail
+    // launches at 4096), and never for gate/up (2 x 4 waves of 3 row tiles: not pairs).
+    if (kTileCand[i].bn == 192 && (I8 || glu)) continue;
     const int64_t blocks = ceil_div(M, kTileCand[i].bm) * ceil_div(N, kTileCand[i].bn);
     const double cost = (double)ceil_div(blocks, (int64_t)cus) * tile_round_cost<I8>(i);
     if (cost < best_cost * 0.999) {

@@ -143,9 +143,9 @@ def test_llama_shapes_at_4096_tokens(pkg, dev, k, n):
 
 @pytest.mark.parametrize("m,n", [(1500, 6000), (2048, 6144)])
 def test_tiled_192_row_tiles_bit_exact(pkg, dev, m, n):
-    """The 256 x 192 tile the model picks for 6000 and 6144 rows at 1500 and 2048 tokens (on 256
-    CUs), with a last block of 3 row tiles for 6000: accumulators exactly against an fp64 GEMM on
-    the GPU, outputs against the oracle's epilogue."""
+    """The shapes for which W8A16 takes 256 x 192 tiles (6000 and 6144 rows at 1500 and 2048
+    tokens), in W8A8, which keeps the other tiles there: accumulators exactly against an fp64
+    GEMM on the GPU, outputs against the oracle's epilogue."""
     k = 4096
     x_bits, w = ora.seeded_inputs(1930 + m + n, m, n, k, outliers=True)
     q, s = pkg.ops.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
