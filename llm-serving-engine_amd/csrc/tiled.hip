@@ -467,6 +467,10 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
     }
   }
   if constexpr (!I8) {
+    // 96 x 128 (65..96 tokens, one block row, so the weights stream with nt): four waves of
+    // 96 x 32.
+    if (sh.bm == 96)
+      return reinterpret_cast<const void*>(&tiled_gemm_kernel<false, 96, 128, 1, 4, 4, GLU, true>);
     // 64 x 128 (narrow prefill; 33..64 tokens over a wide weight, launch_w8a16_wide_decode) and
     // 32 x 128 (17..32 tokens over a wide weight): four waves of BM x 32.
     if (sh.bm == 64)
@@ -505,11 +509,16 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
 // round of 256 blocks at M = 2048: on MI355X W8A16 97.6 us there against 103-114 us for the
 // 128 x 128 tiles, 0.92 of the 256 x 256 tile's rate at M = 8192. Only W8A16 non-gate/up
 // launches consider it (tiled_shape).
-constexpr int kTileCands = 6;
+// The 96 x 128 tile (four waves of 96 x 32, W8A16) holds 65..96 tokens in one block row with
+// a quarter less padding than 128 x 128: on MI355X over gate_up (K 4096, N 28672) at 65 / 80 / 96
+// tokens 36-37 / 33.5 / 33.8 us against 38.3 / 38.5 / 39.5 us, fused gate_up 31.5-32.6 against
+// 37.6-38.8 us. Measured only there, so only launches of one such block row consider it.
+constexpr int kTileCands = 7;
 constexpr TiledShape kTileCand[kTileCands] = {{256, 256}, {256, 128}, {128, 256}, {128, 128},
-                                              {64, 128},  {256, 192}};
-constexpr double kTileEff16[kTileCands] = {1.0, 0.86, 0.87, 0.835, 0.6, 0.92};
-constexpr double kTileEff8[kTileCands] = {1.0, 0.81, 0.865, 0.86, 0.6, 0.926};  // 256 x 192 unused
+                                              {64, 128},  {256, 192}, {96, 128}};
+constexpr double kTileEff16[kTileCands] = {1.0, 0.86, 0.87, 0.835, 0.6, 0.92, 0.75};
+// (256 x 192 and 96 x 128 serve W8A16 only.)
+constexpr double kTileEff8[kTileCands] = {1.0, 0.81, 0.865, 0.86, 0.6, 0.926, 0.75};
 
 // One round of candidate i on every CU, in the cost model's units.
 template <bool I8>
@@ -526,6 +535,7 @@ static TiledShape tiled_shape(int64_t M, int64_t N, int cus, double* cost_out = 
     // 256 x 192: W8A16 only (in W8A8 on par at M = 2048, 3-9 % slower than the bulk-and-tail
     // launches at 4096), and never for gate/up (2 x 4 waves of 3 row tiles: not pairs).
     if (kTileCand[i].bn == 192 && (I8 || glu)) continue;
+    if (kTileCand[i].bm == 96 && (I8 || M > 96)) continue;  // W8A16, one block row only
     const int64_t blocks = ceil_div(M, kTileCand[i].bm) * ceil_div(N, kTileCand[i].bn);
     const double cost = (double)ceil_div(blocks, (int64_t)cus) * tile_round_cost<I8>(i);
     if (cost < best_cost * 0.999) {
@@ -555,7 +565,7 @@ static int launch_tiled_range(const TiledShape& sh, bool decode, const void* x, 
                               const int8_t* qp, const float* s, const float* sx, uint16_t* y,
                               int64_t ldy, int32_t* acc, int64_t M, int64_t N, int64_t K,
                               int64_t glu, int64_t n0, int64_t n, hipStream_t stream) {
-  const int threads = sh.bm <= 64 ? 256 : kTiledThreads;
+  const int threads = sh.bm <= 96 ? 256 : kTiledThreads;  // the 96-, 64- and 32-row tiles: 4 waves
   TiledArgs a{};
   a.x = x;
   a.ldx = ldx;

@@ -286,3 +286,18 @@ def test_quantize_model_fuses_the_mlp(pkg, dev):
     scale = logits[None].abs().max().item()
     assert (logits[True] - logits[None]).abs().max().item() <= 0.05 * scale
     assert (logits[True] - logits[False]).abs().max().item() <= 0.02 * scale
+
+
+def test_w8a16_96_row_tiles(pkg, dev):
+    """Fused gate/up at 65..96 tokens in one block row of 96 x 128 tiles (I 8500: 133 blocks of
+    64 gate/up row pairs, the last partly past I): against the oracle at 80 tokens, and row for
+    row the same bits as inside 100 tokens (128 x 128 tiles)."""
+    i, k = 8500, 1024
+    x_bits, q, s = _inputs(9601, 100, i, k)
+    qp, st = _device_weights(pkg, dev, q, s)
+    x = to_bf16_tensor(x_bits, dev)
+    h100 = bf16_bits(pkg.ops.w8a16_glu(x, qp, st, algo=PREFILL))
+    h80 = bf16_bits(pkg.ops.w8a16_glu(x[:80], qp, st, algo=PREFILL))
+    ok, msg = ora.within_tolerance(h80, ora.w8a16_glu_golden(x_bits[:80], q, s))
+    assert ok, msg
+    np.testing.assert_array_equal(h80, h100[:80])

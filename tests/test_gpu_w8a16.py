@@ -345,6 +345,24 @@ def test_llama_prefill_shapes_full_size(pkg, dev, k, n):
         assert ok, f"M={m} K={k} N={n}: {msg}"
 
 
+def test_prefill_96_row_tiles(pkg, dev):
+    """65..96 tokens over a wide weight run in one block row of 96 x 128 tiles (N 17000: 133
+    blocks, the last with 8 of its rows; K 1040: a 16-wide tail): against the oracle at 65 and 96
+    tokens, and row for row the same bits as the same rows inside 100 tokens (128 x 128 tiles)."""
+    n, k = 17000, 1040
+    x_bits, w = ora.seeded_inputs(9600, 100, n, k)
+    q, s = ora.quantize_weight_per_channel(w)
+    x = to_bf16_tensor(x_bits, dev)
+    qp = pkg.ops.pack_weight(torch.from_numpy(q).to(dev))
+    st = torch.from_numpy(s).to(dev)
+    y100 = bf16_bits(pkg.ops.w8a16_linear(x, qp, st, algo=PREFILL))
+    for m in (65, 96):
+        y = bf16_bits(pkg.ops.w8a16_linear(x[:m], qp, st, algo=PREFILL))
+        ok, msg = ora.within_tolerance(y, ora.w8a16_golden(x_bits[:m], q, s))
+        assert ok, f"M={m}: {msg}"
+        np.testing.assert_array_equal(y, y100[:m])
+
+
 @pytest.mark.parametrize("m,n", [(1500, 6000), (2048, 6144)])
 def test_prefill_192_row_tiles(pkg, dev, m, n):
     """6000 and 6144 rows at 1500 and 2048 tokens: on 256 CUs the tile model picks 256 x 192
