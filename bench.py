@@ -296,7 +296,9 @@ def bench_w8a8(pkg, dev, steps: int, gen) -> dict:
     "layer"), at M in W8A8_MS. LAYERS weight copies are rotated (8 x 218 MB, beyond the 256 MB
     Infinity Cache) and the calls replayed from one captured graph, so the HBM-bound small-M
     figures are GPU time, not host launch time. Reports TOP/s (2MNK), ms per layer and GB/s of
-    algorithmic bytes (quantizer 3MK + 4M, GEMM K·N + 4N + MK + 4M + 2MN)."""
+    algorithmic bytes (quantizer 3MK + 4M, GEMM K·N + 4N + MK + 4M + 2MN), and from M = 512
+    `gemm_tops`: the int8 GEMM with its epilogue alone on x quantized beforehand, the work the
+    vendor GEMM figure times."""
     import torch
 
     weights = [make_weights(pkg, dev, k, n, LAYERS, gen) for k, n in SHAPES]
@@ -320,6 +322,20 @@ def bench_w8a8(pkg, dev, steps: int, gen) -> dict:
         t = time_graph(step, max(2, steps // 4)) / LAYERS
         res[str(m)] = {"tops": round(ops / t / 1e12, 2), "ms": round(t * 1e3, 4),
                        "gbps": round(nbytes / t / 1e9, 1)}
+        if m >= 512:
+            # The int8 GEMM and its epilogue alone (x quantized beforehand), the same work as
+            # the vendor GEMM timed below, plus the bf16 epilogue.
+            xqs = [pkg.ops.quantize_act_per_token(x) for x in xs]
+
+            def gemm_step(xqs=xqs):
+                for layer in range(LAYERS):
+                    for (xq, sx), copies in zip(xqs, weights):
+                        q, s = copies[layer]
+                        pkg.ops.w8a8_gemm(xq, sx, q, s)
+
+            tg = time_graph(gemm_step, max(2, steps // 4)) / LAYERS
+            res[str(m)]["gemm_tops"] = round(ops / tg / 1e12, 1)
+            del xqs
     del weights
     # Context, not the product: the vendor BLAS's int8 GEMM (torch._int_mm, int32 out, no
     # quantizer or epilogue) on the same shapes at the prefill-sized M, rotated copies.
