@@ -26,6 +26,9 @@
 //    reads of 16 rows at one K offset have no LDS bank conflicts (tiled_swz).
 //  * One barrier per stage: after it, the stage's loads from every wave have landed and every
 //    wave has finished reading the slot the next loads overwrite.
+//  * Output: each lane stores its four bf16 of a 16 x 16 tile directly (8 bytes), except in
+//    W8A16 256 x 256 launches of three or more rounds of blocks, where the block's tile is staged
+//    in the stage ring once the K loop is done and written as whole rows (STAGE_Y).
 //
 // Tile order. Blocks are dispatched round-robin over the 8 XCDs; the tile index is remapped so
 // each XCD runs a contiguous range of tiles, in groups of kGroupM token blocks x consecutive
@@ -89,11 +92,12 @@ __device__ __forceinline__ int tiled_swz(int r) {
 // tile layout, whose two 1 KB halves are the lo / hi operands an int8 tile dequantizes to: the
 // tiles are read from LDS as they are, with no scales, y = bf16(sum).
 template <bool I8, int BM, int BN, int WGM, int WGN, int NST, bool GLU, bool NT = false,
-          bool BFW = false>
+          bool BFW = false, bool STAGE_Y = false>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 tiled_gemm_kernel(TiledArgs a) {
   using Acc = std::conditional_t<I8, i32x4, f32x4>;
   static_assert(!BFW || (!I8 && !GLU), "bf16 weights: plain W16A16 only");
+  static_assert(!STAGE_Y || (!I8 && !GLU && !BFW), "staged output: plain W8A16 only");
   constexpr int W = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -119,10 +123,13 @@ tiled_gemm_kernel(TiledArgs a) {
   // rows (2 x 4) it measured 3-5 % slower, so those keep the plain schedule.
   constexpr bool WAHEAD = !I8 && !BFW && WGM == 1;
 
-  // One LDS array per stage slot (x image, then the weight tiles and their padding).
+  // One LDS array per stage slot (x image, then the weight tiles and their padding); with
+  // STAGE_Y one array of all NST slots, which the epilogue reuses for the block's output tile.
   constexpr int SLOT = (XBYTES + WI * W * 1024) / 16;
-  __shared__ uint4 st0[SLOT], st1[SLOT], st2[SLOT], st3[NST > 3 ? SLOT : 1];
+  __shared__ uint4 st0[STAGE_Y ? NST * SLOT : SLOT], st1[STAGE_Y ? 1 : SLOT],
+      st2[STAGE_Y ? 1 : SLOT], st3[!STAGE_Y && NST > 3 ? SLOT : 1];
   auto xslot = [&](int i) -> uint4* {
+    if constexpr (STAGE_Y) return st0 + i * SLOT;
     switch (i) {
       case 0: return st0;
       case 1: return st1;
@@ -399,6 +406,47 @@ tiled_gemm_kernel(TiledArgs a) {
     }
     return;
   }
+  if constexpr (STAGE_Y) {
+    // The block's bf16 tile goes through LDS (rows padded by 16 bytes, which spreads the
+    // 16-row column writes over the banks) and out as whole rows of 16-byte stores. Same values
+    // as the direct stores below, which remain for a y not 16-byte aligned row by row.
+    constexpr int YROW = BN * 2 + 16;
+    static_assert(BM * YROW <= NST * SLOT * 16, "the output tile fits the stage ring");
+    if (a.y && (a.ldy & 7) == 0 && ((uintptr_t)a.y & 15) == 0) {
+      char* ys = reinterpret_cast<char*>(st0);
+      __syncthreads();  // every wave's reads of the ring have completed (loads drained above)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int ml = wm * WM + 16 * i + r16;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int nl = wn * WN + 16 * j + 4 * g, n = n0 + nl;
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            o[r] = scaled<false>(acc[i][j], r, n + r < a.N ? a.s[n + r] : 0.0f, 0.0f);
+          *reinterpret_cast<uint2*>(ys + ml * YROW + nl * 2) =
+              make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+        }
+      }
+      __syncthreads();
+      constexpr int CPR = BN / 8;  // 16-byte chunks per row
+      const int cols = min(BN, a.N - n0);
+      for (int c = threadIdx.x; c < BM * CPR; c += 64 * W) {
+        const int r = c / CPR, nl = 8 * (c % CPR);
+        if (r >= rows || nl >= cols) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(ys + r * YROW + nl * 2);
+        uint16_t* out = a.y + (int64_t)(m0 + r) * a.ldy + n0 + nl;
+        if (nl + 8 <= cols) {
+          *reinterpret_cast<uint4*>(out) = v;
+        } else {
+          const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+          for (int t = 0; t < cols - nl; ++t) out[t] = e[t];
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int m = m0 + wm * WM + 16 * i + r16;
@@ -450,9 +498,18 @@ static const void* tiled_fn() {
 // 28.3 -> 25.6 us), plain W8A16 gate_up -5 % to +4 %; in the bench's mid-range figures (random
 // activations) W8A8 gate_up 2-4 % faster and W8A16 unchanged. With two block rows (M > 128) nt
 // measured 8-14 % slower.
+//
+// `stage_y`: a W8A16 256 x 256 launch (no gate/up) of at least kStageYRounds rounds of blocks,
+// whose output tiles go out through LDS as whole rows (STAGE_Y). Measured on MI355X against the
+// direct stores, bit-identical: q/k/v at M = 8192 (3 rounds) 319 -> 311 us, gate_up at 8192 (14
+// rounds) 1460 -> 1425 us, at 2048 (3.5 rounds) 410 -> 397 us; with one or two rounds unchanged
+// or up to 1 % slower (o_proj, down_proj at 8192; at one K step 22.9 -> 30.6 us), and no gain
+// in W8A8.
+constexpr int kStageYRounds = 3;
+
 template <bool I8, bool GLU>
 static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
-                                    bool one_row = false) {
+                                    bool one_row = false, bool stage_y = false) {
   if (decode) {
     if constexpr (!I8) {
       if (sh.bm == 64)
@@ -483,7 +540,14 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
     if (sh.bm == 64)
       return reinterpret_cast<const void*>(&tiled_gemm_kernel<true, 64, 128, 2, 2, 4, GLU>);
   }
-  if (sh.bm == 256 && sh.bn == 256) return tiled_fn<I8, 256, 256, GLU>();
+  if (sh.bm == 256 && sh.bn == 256) {
+    if constexpr (!I8 && !GLU) {
+      if (stage_y)
+        return reinterpret_cast<const void*>(
+            &tiled_gemm_kernel<false, 256, 256, 1, 8, 3, false, false, false, true>);
+    }
+    return tiled_fn<I8, 256, 256, GLU>();
+  }
   if (sh.bm == 256 && sh.bn == 192) {
     if constexpr (I8 || GLU) return nullptr;  // W8A16 without gate/up only (tiled_shape)
     else return tiled_fn<false, 256, 192, false>();
@@ -588,8 +652,10 @@ static int launch_tiled_range(const TiledShape& sh, bool decode, const void* x, 
   if (blocks > 0x7fffffff) return LSE_E_RANGE;
   void* args[] = {&a};
   const bool one_row = a.mblocks == 1;
+  const bool stage_y = !I8 && glu == 0 && !decode && sh.bm == 256 && sh.bn == 256 &&
+                       blocks >= (int64_t)kStageYRounds * device_cus();
   const void* fn = glu > 0 ? tiled_kernel_for<I8, true>(sh, decode, one_row)
-                            : tiled_kernel_for<I8, false>(sh, decode, one_row);
+                            : tiled_kernel_for<I8, false>(sh, decode, one_row, stage_y);
   if (!fn) return LSE_E_RANGE;
   const hipError_t e =
       hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(threads), args, 0, stream);

@@ -412,3 +412,44 @@ def test_tail_split_launch_changes_no_bit(pkg, dev, mode, n, m):
         run = lambda xx: pkg.ops.w8a16_linear(xx, qp, s, algo=PREFILL)  # noqa: E731
     a, b = run(x[:m]), run(x)
     assert torch.equal(a.view(torch.int16), b[:m].view(torch.int16))
+
+
+def _abi_prefill(pkg, dev, x, qp, s, n, ldy):
+    """The tiled GEMM through the C ABI into an (M, ldy) buffer; the columns past n must stay
+    untouched."""
+    m, k = x.shape
+    out = torch.full((m, ldy), -7.0, dtype=torch.bfloat16, device=dev)
+    ws = pkg.ops.workspace(0, m, n, k, dev)
+    status = pkg.library().lse_w8a16_gemm_algo(
+        x.data_ptr(), k, qp.data_ptr(), s.data_ptr(), out.data_ptr(), ldy, m, n, k, PREFILL,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        torch.cuda.current_stream().cuda_stream)
+    assert status == 0
+    torch.cuda.synchronize()
+    assert torch.all(out[:, n:] == -7.0), "kernel wrote outside y's rows"
+    return out[:, :n]
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 28672, 4096), (8192, 6144, 4096), (8000, 6140, 1024)])
+def test_staged_output_tiles_bit_identical(pkg, dev, m, n, k):
+    """W8A16 256 x 256 launches of three or more rounds of blocks on 256 CUs (gate_up at 2048
+    tokens: 768 blocks in its full rounds; 6144 rows at 8192: 768; 8000 x 6140: 768, the last
+    block row 64 tokens, the last block column 252 rows, a partial 16-byte chunk) stage each
+    output tile through LDS when y's rows are 16-byte aligned (row stride a multiple of 8) and
+    store it directly otherwise. Both give the same bits; the ragged case also against the fp64
+    product on the GPU."""
+    gen = torch.Generator(device="cpu").manual_seed(5150 + m + n)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
+    q, s = pkg.ops.quantize_weight_per_channel(w)
+    del w
+    qp = pkg.ops.pack_weight(q)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+    ld_staged = (n + 8) // 8 * 8
+    ld_direct = ld_staged + 4
+    a = _abi_prefill(pkg, dev, x, qp, s, n, ld_staged)
+    b = _abi_prefill(pkg, dev, x, qp, s, n, ld_direct)
+    assert torch.equal(a.contiguous().view(torch.int16), b.contiguous().view(torch.int16))
+    if n % 8:
+        golden = (x.double() @ q.double().t()) * s.double()[None, :]
+        ok, msg = check_rows_in_chunks(a.contiguous(), golden)
+        assert ok, f"M={m} N={n}: {msg}"
