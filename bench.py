@@ -913,17 +913,22 @@ def summarize_prefill(trace_dir: str, pmc_dir: str) -> None:
 def summarize_w8a8(trace_dir: str, pmc_dir: str) -> None:
     """Per (M, shape) duration, TOP/s and int8 MFMA utilisation of the W8A8 tiled GEMM at the
     prefill-sized M of config 3, from a kernel trace and a counter run of `bench.py --only w8a8`
-    (each M runs one eager pass, then three graph replays at `--steps 8`, LAYERS passes each,
-    every pass the four shapes in order; the decode-range M use other kernels and are left
-    out)."""
+    (each M runs the quantizer + GEMM step, then the GEMM alone on x quantized beforehand
+    (`gemm_tops`), each as one eager pass and three graph replays at `--steps 8`, LAYERS passes
+    each, every pass the four shapes in order: 8 LAYERS passes of the same GEMM kernels; the
+    decode-range M use other kernels and are left out)."""
     def prefill_gemm(name: str) -> bool:  # the int8 tiled GEMM with the default cache policy
         head = name.split("(")[0]
-        return "tiled_gemm_kernel<true" in head and head.endswith("false, false>")
+        if "tiled_gemm_kernel<" not in head:
+            return False
+        # template arguments: I8, BM, BN, WGM, WGN, NST, GLU, NT (streaming loads), BFW, STAGE_Y
+        targs = [t.strip() for t in head[head.index("<") + 1:head.rindex(">")].split(",")]
+        return targs[0] == "true" and targs[7] == "false"
 
     ms = [m for m in W8A8_MS if m > 64]
     rows = []
     for m, sn, k, n, name, us, insts, busy, cycles in tiled_calls(
-            trace_dir, pmc_dir, prefill_gemm, ms, 64, 4 * LAYERS):
+            trace_dir, pmc_dir, prefill_gemm, ms, 64, 8 * LAYERS):
         rows.append((m, sn, k, n, name, us, 2.0 * m * n * k / us / 1e6, insts, busy,
                      cycles / us / 1e3, busy / (CUS * SIMDS_PER_CU * cycles)))
     cmds = [
