@@ -33,6 +33,7 @@ Profiling (the decode sweep alone, then a CPU-side summary of the rocprofv3 outp
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import sys
 from pathlib import Path
@@ -53,6 +54,7 @@ LAYERS = 8
 CALIBRATION_BYTES = 64 << 20
 PROFILE_MD = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.md"
 PROFILE_TRAFFIC = REPO_ROOT / "profiles" / "skinny_kernel_decode_sweep.traffic.json"
+CSRC = REPO_ROOT / "llm-serving-engine_amd" / "csrc"
 PROFILE_PREFILL = REPO_ROOT / "profiles" / "tiled_gemm_kernel_prefill.md"
 PROFILE_W8A8 = REPO_ROOT / "profiles" / "tiled_gemm_kernel_w8a8.md"
 PROFILE_GLU = REPO_ROOT / "profiles" / "fused_gate_up_kernels.md"
@@ -794,6 +796,7 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> None:
         "fetch_factor": round(ff, 4),
         "write_factor": round(wf, 4),
         "median_us_per_call": round(avg_t, 3),
+        "library_sources_sha16": library_sources_digest(),
     }, indent=1) + "\n")
     print("\n".join(out))
 
@@ -1124,15 +1127,29 @@ def collections_by_dispatch(rows: list[dict], kernel: str) -> list[dict]:
     return [by[d] for d in sorted(by)]
 
 
-def measured_traffic(dec: dict) -> float | None:
-    """HBM bytes per decode call from the committed PMC summary of this same sweep, or None."""
+def library_sources_digest() -> str:
+    """First 16 hex digits of the SHA-256 over the HIP sources (file names and contents, sorted):
+    a PMC traffic figure is only reported for the library build it was measured on."""
+    h = hashlib.sha256()
+    for f in sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")):
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(dec: dict) -> tuple[float | None, str]:
+    """(HBM bytes per decode launch from the committed PMC summary of this same sweep, or None;
+    why None). The summary counts only if it covers the same launches and was measured on a
+    library built from the current sources."""
     try:
         t = json.loads(PROFILE_TRAFFIC.read_text())
     except (OSError, ValueError):
-        return None
+        return None, f"no readable {PROFILE_TRAFFIC.name}"
     if t.get("calls") != dec["launches_per_step"]:
-        return None
-    return t["hbm_bytes_per_call"]
+        return None, "the PMC summary covers another set of launches"
+    if t.get("library_sources_sha16") != library_sources_digest():
+        return None, "the PMC summary was measured on another build of the kernels"
+    return t["hbm_bytes_per_call"], ""
 
 
 def bench_eager_overhead(pkg, dev, steps: int, gen, calls: int = 500) -> dict:
@@ -1420,6 +1437,7 @@ def main() -> None:
         }
 
     gbps = dec["gbps"]
+    traffic, why = measured_traffic(dec)
     out = {
         "metric": "HBM GB/s at decode M<=64 + TOPS at prefill M=2048, Llama-3-8B int8 linears",
         "value": round(gbps, 1),
@@ -1440,13 +1458,20 @@ def main() -> None:
             "launches_per_step": dec["launches_per_step"],
             "bytes_per_step": dec["bytes_per_step"],
         },
-        "roofline": {
+        "roofline": {  # the decode launches: per-launch algorithmic bytes / average duration
             "bound": "hbm",
             "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic(dec),
+            "traffic": traffic,
+            "traffic_unit": "HBM bytes per launch, mean over the sweep's launches",
+            "traffic_source": (f"profiles/{PROFILE_TRAFFIC.name}: rocprofv3 --pmc FETCH_SIZE and "
+                               "--pmc WRITE_SIZE runs of this sweep, each scaled by its reading "
+                               "for a plain 64 MiB copy" if traffic is not None else why),
+            "algorithmic_bytes_per_launch": round(dec["bytes_per_step"]
+                                                  / dec["launches_per_step"]),
+            "avg_launch_us": round(dec["seconds_per_step"] / dec["launches_per_step"] * 1e6, 3),
         },
         "cpu_baseline": cpu,
         "cpu_int8_restatements": cpu_int8,

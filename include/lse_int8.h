@@ -29,12 +29,16 @@
  *  - Return value: LSE_OK (0) on success; a negative LSE_E_* code for a rejected argument
  *    (nothing was launched); a positive hipError_t from the launch otherwise.
  *  - Results are deterministic: no atomics, and the summation order of every output element
- *    depends only on N, K, the device's CU count and the token class of the call (M <= 16,
- *    17..32, 33..64, 65..128, 129..256, > 256), never on M inside the class, on other rows or on
- *    timing. Row m of y is therefore bit-identical whether it is computed alone or inside a
- *    padded batch of the same class. The classes align with power-of-two decode buckets
- *    (bucket(M) <= 16 exactly when M <= 16, and so on), so a graphed bucket and the eager batch
- *    it stands for compute each row identically.
+ *    depends only on N, K, the device's CU count and the token class of the call, never on M
+ *    inside the class, on other rows or on timing. Row m of y is therefore bit-identical whether
+ *    it is computed alone or inside a padded batch of the same class. W8A8 sums are exact int32,
+ *    so its rows are identical for every M. The W8A16 classes are M <= 16, 17..32, 33..64,
+ *    65..128 and 129..256, and above 256 tokens one class, except over a deep, narrow weight
+ *    (at least 128 K steps of 64, i.e. K > 8128, and few enough output tiles that the split grid
+ *    fits the CUs: down_proj of Llama-3-8B on 256 CUs), where 257..512, 513..1024 and > 1024 are
+ *    three. The classes align with power-of-two decode buckets (bucket(M) <= 16 exactly when
+ *    M <= 16, and so on), so a graphed bucket and the eager batch it stands for compute each
+ *    row identically; a caller that pads a batch must pad within its class.
  */
 #ifndef LSE_INT8_H
 #define LSE_INT8_H
@@ -137,7 +141,9 @@ int lse_w8a16_gemm(const void* x, int64_t ldx, const int8_t* qp, const float* s,
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls
  * no hipMalloc, hipFree or allocating routine: the workspace lse_w8a16_gemm would take lives in a
  * static device array of LSE_NOALLOC_SCRATCH_BYTES (32 MiB) that each device the library runs on
- * holds until the process ends, its device address looked up on the device's first call. Same
+ * holds until the process ends, its device address looked up on the device's first call. A
+ * call with M = 0 launches nothing and only does that lookup for the current device: a caller
+ * whose first real call on a device is made under HIP graph capture makes one before it. Same
  * kernels, so y is bit-identical to lse_w8a16_gemm's. Calls that overlap on one device (two
  * streams at once) share that array and race; calls in stream order do not. Returns
  * LSE_E_SCRATCH when lse_workspace_bytes(LSE_MODE_W8A16, M, N, K) exceeds the array.

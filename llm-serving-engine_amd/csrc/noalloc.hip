@@ -7,9 +7,11 @@
 // Each device holds its own copy of `scratch` at its own address, kept until the process ends.
 // In host code the array's name is only a host-side stand-in, so its device address is looked up
 // once per device with hipGetSymbolAddress, with that device current, and only that address is
-// ever passed to a kernel. Every call on a device shares the device's array and leaves the last
-// call's partial sums in it: calls that overlap on one device (two streams at once) race. Nothing
-// needs clearing between calls: each call writes every partial sum it reads before reading it.
+// ever passed to a kernel; a call with M = 0 does only that lookup, for callers that capture
+// their first real call into a graph. Every call on a device shares the device's array and
+// leaves the last call's partial sums in it: calls that overlap on one device (two streams at
+// once) race. Nothing needs clearing between calls: each call writes every partial sum it reads
+// before reading it.
 #include <mutex>
 
 #include "lse_common.h"
@@ -51,7 +53,10 @@ int lse_w8a16_gemm_noalloc(const void* x, int64_t ldx, const int8_t* qp, const f
   if (need < 0) return LSE_E_SHAPE;
   if (need > kScratchBytes) return LSE_E_SCRATCH;
   void* ws = nullptr;
-  if (M > 0 && N > 0) {
+  // A call with M = 0 launches nothing and only looks the current device's address up, so a
+  // caller can do that before it starts a graph capture.
+  if (M == 0) return device_scratch(&ws);
+  if (N > 0) {
     if (int st = device_scratch(&ws)) return st;
   }
   return lse_w8a16_gemm(x, ldx, qp, s, y, ldy, M, N, K, need > 0 ? ws : nullptr, need, stream);

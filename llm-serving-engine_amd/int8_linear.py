@@ -152,11 +152,21 @@ class QKVGroup:
     (same tensor version), and the result is dropped once all three have taken their columns.
     Any other call computes the stacked product afresh. Each module's output is a column view of
     the (..., Nq + Nk + Nv) product, bit-identical to what the stacked weight gives for those
-    columns."""
+    columns.
+
+    Inference tensors (`torch.inference_mode`) carry no version counter, so for them a hit needs
+    the same input object only: the input must not be rewritten in place between the three calls
+    (the runner never does), and neither may any tensor be written through its data pointer (a
+    HIP kernel's output) between them, which no version counter sees either.
+
+    Moving or reloading the modules (`Module._apply`, `load_state_dict(assign=True)`) replaces
+    their buffers with tensors that are no longer views of the stacked ones; the next call that
+    computes the product notices and stacks the members' current buffers again."""
 
     def __init__(self, qweight: torch.Tensor, scales: torch.Tensor, mode: str,
                  members: list[Int8Linear]) -> None:
         self.qweight, self.scales, self.mode = qweight, scales, mode
+        self.members = list(members)
         self.n = int(scales.shape[0])
         self.offsets: dict[int, tuple[int, int]] = {}
         at = 0
@@ -169,14 +179,39 @@ class QKVGroup:
         self._pending: set[int] = set()
 
     @staticmethod
-    def _version_of(x) -> int:
-        return (x.xq if isinstance(x, QuantizedRows) else x)._version
+    def _version_of(x) -> int | None:
+        t = x.xq if isinstance(x, QuantizedRows) else x
+        return None if t.is_inference() else t._version
+
+    def _members_are_views(self) -> bool:
+        """Whether every member's buffers are still its rows of the stacked weight and scales."""
+        row = self.qweight.stride(0)
+        for mod in self.members:
+            a, _ = self.offsets[id(mod)]
+            qw, sc = mod._buffers["qweight"], mod._buffers["scales"]
+            if (qw.device != self.qweight.device or sc.device != self.scales.device
+                    or qw.data_ptr() != self.qweight.data_ptr() + (a // 16) * row
+                    or sc.data_ptr() != self.scales.data_ptr() + 4 * a
+                    or sc.dtype != torch.float32):
+                return False
+        return True
+
+    def _restack(self) -> None:
+        """Stacks the members' current buffers again and makes them views of the result."""
+        self.qweight = torch.cat([m._buffers["qweight"] for m in self.members])
+        self.scales = torch.cat([m._buffers["scales"].float() for m in self.members])
+        for m in self.members:
+            a, b = self.offsets[id(m)]
+            m._buffers["qweight"] = self.qweight[a // 16:b // 16]
+            m._buffers["scales"] = self.scales[a:b]
 
     def columns(self, mod: Int8Linear, x) -> torch.Tensor:
         key = id(mod)
         hit = (self._out is not None and x is self._input and key in self._pending
                and self._version_of(x) == self._version)
         if not hit:
+            if not self._members_are_views():
+                self._restack()
             self._out = _int8_product(self.mode, x, self.qweight, self.scales, self.n)
             self._input, self._version = x, self._version_of(x)
             self._pending = set(self.offsets)

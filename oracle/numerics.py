@@ -125,13 +125,6 @@ def w8a8_epilogue(acc: np.ndarray, sx: np.ndarray, s: np.ndarray) -> np.ndarray:
     return f32_to_bf16_bits(y.astype(np.float32))
 
 
-def bf16_linear_cpu(x_bits: np.ndarray, w: np.ndarray) -> np.ndarray:
-    """fp64 product x·Wᵀ of the unquantized layer (the reference's bf16 `F.linear`,
-    torch/nn/modules/linear.py:134), with W rounded to bf16 as the reference stores it."""
-    wb = bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(w, np.float32))).astype(np.float64)
-    return bf16_bits_to_f32(x_bits).astype(np.float64) @ wb.T
-
-
 def within_tolerance(y_bits: np.ndarray, golden: np.ndarray, rel: float = 1e-2) -> tuple[bool, str]:
     """The W8A16 acceptance rule: max-abs error <= rel * max|golden|, and elementwise relative
     error <= rel wherever |golden| > 1e-3 * max|golden|."""

@@ -250,3 +250,59 @@ def test_quantized_llama_groups_every_layer(pkg, dev):
     with torch.no_grad():
         a, b = grouped(ids).logits.float(), plain(ids).logits.float()
     assert ((a - b).norm() / b.norm()) < 1e-2
+
+
+def _tiny_llama(pkg, dev, mode, seed=5):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=96, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64,
+                      bos_token_id=None, eos_token_id=None, pad_token_id=None)
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        return pkg.quantize_model_(
+            LlamaForCausalLM._from_config(cfg, dtype=torch.bfloat16).eval(), mode)
+
+
+@pytest.mark.parametrize("mode", ["int8", "w8a8"])
+def test_grouped_qkv_and_quantized_llama_under_inference_mode(pkg, dev, mode):
+    """Serving stacks run under torch.inference_mode(), whose tensors carry no version counter:
+    the grouped q/k/v still serve the three calls from one stacked GEMM, and a quantized Llama
+    forward gives the same logits as under no_grad (the reference's mode)."""
+    from llm_serving_engine_amd.int8_linear import group_qkv
+
+    attn = _attention_projections(pkg, dev, mode)
+    group_qkv(attn)
+    with torch.inference_mode():
+        x = torch.randn(7, 256, device=dev).to(torch.bfloat16)
+        assert x.is_inference()
+        q, k, v = attn.q_proj(x), attn.k_proj(x), attn.v_proj(x)
+        assert q.untyped_storage().data_ptr() == v.untyped_storage().data_ptr()
+        stacked = (pkg.ops.w8a16_linear(x, attn.q_proj.__dict__["_qkv_group"].qweight,
+                                        attn.q_proj.__dict__["_qkv_group"].scales)
+                   if mode == "int8" else None)
+    if stacked is not None:
+        assert torch.equal(torch.cat([q, k, v], -1), stacked)
+    model = _tiny_llama(pkg, dev, mode)
+    ids = torch.randint(0, 96, (2, 11), device=dev)
+    with torch.no_grad():
+        ref = model(ids).logits
+    with torch.inference_mode():
+        got = model(ids).logits
+    assert torch.equal(got, ref)
+
+
+def test_grouped_qkv_survives_a_device_round_trip(pkg, dev):
+    """Module._apply (model.to(...)) replaces the grouped modules' buffers with tensors that are
+    no longer views of the stacked weight; the group stacks them again and the logits do not
+    change."""
+    model = _tiny_llama(pkg, dev, "int8", seed=9)
+    ids = torch.randint(0, 96, (1, 9), device=dev)
+    with torch.no_grad():
+        before = model(ids).logits
+        model.to("cpu").to(dev)
+        group = model.model.layers[0].self_attn.q_proj.__dict__["_qkv_group"]
+        assert not group._members_are_views()
+        after = model(ids).logits
+    assert group._members_are_views() and group.qweight.device.type == "cuda"
+    assert torch.equal(after, before)

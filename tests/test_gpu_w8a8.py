@@ -222,3 +222,40 @@ def test_wide_weight_tiles_bit_exact(pkg, dev, m):
     """17..64 tokens over a weight of more than 1024 row tiles take 64 x 128 tiles of the tiled
     kernel: accumulators and outputs stay bit-exact, with a partial last tile and a K tail."""
     _check(pkg, dev, m, 16408, 80, 4100 + m)
+
+
+@pytest.mark.parametrize("k,n", LLAMA_SHAPES)
+def test_one_launch_route_at_llama_shapes(pkg, dev, k, n):
+    """The one-launch W8A8 route (`lse_w8a8_linear`) at full Llama-3-8B size, for every M at
+    which `w8a8_linear` takes it by default: 1, 2 and 3 rows at K = 4096 (o_proj and q/k/v at
+    decode, model_runner.py:322-324,369) and 1 row at K = 14336 (down_proj,
+    modeling_llama.py:175). The kernel keeps xq and sx to itself, so they are checked through
+    what they determine: the quantizer of the two-step route equals the oracle's bit for bit,
+    the one-launch accumulators equal the exact integer GEMM of the oracle's xq with q (fp64 on
+    the GPU: integer sums below 2^53 are exact), and y equals the oracle's epilogue of those
+    accumulators with the oracle's sx."""
+    ms = [m for m in (1, 2, 3) if m * k <= pkg.ops.ONE_LAUNCH_W8A8_MAX_ELEMS]
+    assert ms == ([1, 2, 3] if k == 4096 else [1])
+    x_bits, w = ora.seeded_inputs(4400 + k + n, max(ms), n, k, outliers=True)
+    x_bits[min(1, max(ms) - 1), :: 977] = 0  # a row with scattered zeros among the outliers
+    q, s = pkg.ops.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    del w
+    qp = pkg.ops.pack_weight(q)
+    s_host = s.cpu().numpy()
+    for m in ms:
+        assert pkg.library().lse_w8a8_linear_supported(m, k)
+        xm = x_bits[:m]
+        xq_ref, sx_ref = ora.quantize_act_per_token(xm)
+        xq2, sx2 = pkg.ops.quantize_act_per_token(to_bf16_tensor(xm, dev))
+        np.testing.assert_array_equal(xq2.cpu().numpy(), xq_ref)
+        np.testing.assert_array_equal(sx2.cpu().numpy(), sx_ref)
+        y, acc = pkg.ops.w8a8_linear(to_bf16_tensor(xm, dev), qp, s, want_acc=True,
+                                     one_launch=True)
+        torch.cuda.synchronize()
+        xq_t = torch.from_numpy(xq_ref).to(dev)
+        exact = (xq_t.double() @ q.double().t()).round().to(torch.int64)
+        assert torch.equal(acc.to(torch.int64), exact), f"one-launch acc M={m} K={k} N={n}"
+        y_ref = ora.w8a8_epilogue(acc.cpu().numpy(), sx_ref, s_host)
+        np.testing.assert_array_equal(bf16_bits(y), y_ref, err_msg=f"one-launch y M={m}")
+        y2, acc2 = pkg.ops.w8a8_gemm(xq2, sx2, qp, s, True)
+        assert torch.equal(acc, acc2) and torch.equal(y, y2), f"routes differ at M={m}"

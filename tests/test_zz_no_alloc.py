@@ -90,3 +90,39 @@ def test_rejections_before_any_launch(pkg):
     lib = pkg.library()
     assert lib.lse_w8a16_gemm_noalloc(None, 16, None, None, None, 16, -1, 16, 16, None) == -2
     assert lib.lse_w8a16_gemm_noalloc(None, 16, None, None, None, 16, 1, 16, 17, None) != 0
+
+
+def test_captured_split_k_calls_replay_bit_identically(pkg, dev):
+    """A caller under graph capture: one M = 0 call looks the scratch address up first, then
+    down_proj at 24 tokens (split-K decode route) and at 200 (split tiled route) are captured
+    into one graph through the no-alloc entry point and replayed several times, with eager work
+    between the replays; every replay equals lse_w8a16_gemm with a caller workspace."""
+    lib = pkg.library()
+    k, n = 14336, 4096
+    qp, s = _weights(pkg, dev, n, k, 97)
+    gen = torch.Generator().manual_seed(98)
+    xs = {m: torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev) for m in (24, 200)}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert lib.lse_w8a16_gemm_noalloc(None, k, None, None, None, n, 0, n, k,
+                                          side.cuda_stream) == 0
+        outs = {m: torch.empty(m, n, dtype=torch.bfloat16, device=dev) for m in xs}
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream().cuda_stream
+        for m, x in xs.items():
+            st = lib.lse_w8a16_gemm_noalloc(x.data_ptr(), k, qp.data_ptr(), s.data_ptr(),
+                                            outs[m].data_ptr(), n, m, n, k, cap)
+            assert st == 0, lib.lse_status_string(st)
+    stream = torch.cuda.current_stream().cuda_stream
+    for rep in range(3):
+        for m in xs:
+            xs[m].copy_(torch.randn(m, k, generator=gen).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        for m, x in xs.items():
+            ref, _ = _with_workspace(lib, x, qp, s, m, n, k, stream)
+            torch.cuda.synchronize()
+            assert torch.equal(outs[m].view(torch.int16), ref.view(torch.int16)), (rep, m)
