@@ -60,6 +60,7 @@ PROFILE_W8A8 = REPO_ROOT / "profiles" / "tiled_gemm_kernel_w8a8.md"
 PROFILE_GLU = REPO_ROOT / "profiles" / "fused_gate_up_kernels.md"
 PROFILE_ATTN = REPO_ROOT / "profiles" / "paged_attn_kernel_decode.md"
 PROFILE_HEAD = REPO_ROOT / "profiles" / "bf16_lm_head_kernels.md"
+PROFILE_STEP = REPO_ROOT / "profiles" / "decode_step_kernels.md"
 CUS, SIMDS_PER_CU, XCDS = 256, 4, 8
 
 
@@ -75,7 +76,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true", help="skip prefill and W8A8 figures")
     p.add_argument("--only", choices=["decode", "prefill", "w8a8", "glu", "attention",
-                                      "lm-head", "decode-step", "tp8", "mid"],
+                                      "lm-head", "decode-step", "decode-step-linears", "tp8",
+                                      "mid"],
                    help="one family; decode-step is config 4 (a 32-layer model's decode step)")
     p.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE", "FETCH", "WRITE"),
                    help="summarize rocprofv3 output dirs of the decode sweep into profiles/")
@@ -89,6 +91,9 @@ def parse() -> argparse.Namespace:
                    help="write the fused gate_up profile summary from a kernel trace of --only glu")
     p.add_argument("--summarize-w8a8", nargs=2, metavar=("TRACE", "PMC"),
                    help="summarize rocprofv3 output dirs of --only w8a8 into profiles/")
+    p.add_argument("--summarize-decode-step", metavar="TRACE",
+                   help="write the config-4 per-kernel summary from a kernel trace of "
+                        "--only decode-step-linears")
     p.add_argument("--summarize-prefill", nargs=2, metavar=("TRACE", "PMC"),
                    help="summarize rocprofv3 output dirs of --only prefill into profiles/")
     return p.parse_args()
@@ -1073,6 +1078,81 @@ def summarize_lm_head(trace_dir: str, steps: int = 5) -> None:
     print("\n".join(out))
 
 
+def summarize_decode_step(trace_dir: str, steps: int = 20, layers: int = 32) -> None:
+    """Config 4's int8 linear stack by kernel, from a kernel trace of
+    `bench.py --only decode-step-linears --steps 20`: the dispatches after the marker kernel are
+    (steps + 2) passes of one step (an eager pass, a warm-up replay, the timed replays); the
+    last `steps` passes are summarized. Each dispatch is attributed to its projection by its
+    place in the layer's sequence (q/k/v, o_proj, gate/up, down_proj and, when down_proj splits
+    K, its second pass)."""
+    import csv
+
+    with open(Path(trace_dir) / "run_kernel_trace.csv", newline="") as f:
+        trace = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    marks = [i for i, r in enumerate(trace) if DECODE_STEP_MARKER in r["Kernel_Name"]]
+    if not marks:
+        raise RuntimeError(f"no {DECODE_STEP_MARKER} marker in the trace")
+    after = [r for r in trace[marks[-1] + 1:] if "lse::" in r["Kernel_Name"]]
+    if len(after) % (steps + 2):
+        raise RuntimeError(f"{len(after)} dispatches after the marker for {steps + 2} passes")
+    per = len(after) // (steps + 2)
+    if per % layers:
+        raise RuntimeError(f"{per} dispatches per step for {layers} layers")
+    per_layer = per // layers
+    names = ["qkv (4096 -> 6144)", "o_proj (4096 -> 4096)", "gate_up + SiLU-mul (4096 -> 2 x 14336)",
+             "down (14336 -> 4096)", "down, second pass"][:per_layer]
+    timed = after[-steps * per:]
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
+    span = [(int(timed[k * per + per - 1]["End_Timestamp"])
+             - int(timed[k * per]["Start_Timestamp"])) / 1e3 for k in range(steps)]
+    rows: dict[tuple[str, str], list[float]] = {}
+    for k in range(steps):
+        for i in range(per):
+            r = timed[k * per + i]
+            key = (names[i % per_layer], _short(r["Kernel_Name"]).replace("lse::", ""))
+            rows.setdefault(key, []).append(dur(r))
+    total = sum(sum(v) for v in rows.values()) / steps
+    m, hid, inter = 64, 4096, 14336
+    wbytes = {names[0]: 4096 * 6144, names[1]: 4096 * 4096, names[2]: 4096 * 2 * inter,
+              names[3]: inter * 4096}
+    cmds = ["rocprofv3 --kernel-trace --stats -d gpurun_out/prof_step -o run --output-format csv "
+            "-- python3 bench.py --only decode-step-linears --steps 20",
+            "python3 bench.py --summarize-decode-step gpurun_out/prof_step"]
+    out = ["# Config 4: the int8 (W8A16) linear stack of one Llama-3-8B decode step, by kernel, "
+           "one MI355X", "", "Commands (repository root, one MI355X; the last runs on any host):",
+           "", "```", *cmds, "```", "",
+           f"32 layers at M = {m} tokens, captured in one graph; {steps} replays summarized (after "
+           "an eager pass and a warm-up replay). A kernel's time is its trace duration "
+           "(end - start); per step = the sum over its dispatches in one replay, averaged over "
+           "the replays. GB/s = the projection's algorithmic bytes (int8 weights, fp32 scales, "
+           "bf16 activations in and out) per layer / its kernels' time per layer.", "",
+           "| projection | kernel | calls per step | us per call | us per step | share | GB/s |",
+           "|---|---|---|---|---|---|---|"]
+    for (proj, kern), ds in rows.items():
+        calls = len(ds) // steps
+        us_step = sum(ds) / steps
+        gb = ""
+        if proj in wbytes:
+            w = wbytes[proj]
+            n = w // (inter if proj == names[3] else hid)
+            k_in = inter if proj == names[3] else hid
+            n_out = inter if proj == names[2] else n
+            nbytes = w + 4 * n + 2 * m * k_in + 2 * m * n_out
+            layer_us = sum(v for (pp, _), vs in rows.items() if pp == proj for v in vs) / (steps * layers)
+            if proj == names[3] and len(names) > 4:
+                layer_us += sum(v for (pp, _), vs in rows.items() if pp == names[4]
+                                for v in vs) / (steps * layers)
+            gb = f"{nbytes / layer_us / 1e3:.0f}"
+        out.append(f"| {proj} | `{kern}` | {calls} | {us_step / calls:.2f} | {us_step:.1f} | "
+                   f"{us_step / total:.3f} | {gb} |")
+    import statistics
+    out += ["", f"Sum of kernel durations per step: {total:.1f} us; first-to-last dispatch span "
+            f"per replay: median {statistics.median(span):.1f} us (the difference is the gap "
+            "between consecutive kernels in the graph)."]
+    PROFILE_STEP.write_text("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
 def summarize_attention(trace_dir: str) -> None:
     """Kernel-trace durations of `bench.py --only attention`: the paged_attn_kernel dispatches,
     in order, fall into one equal run per ATTN_CASES entry (each case dispatches the same
@@ -1202,6 +1282,34 @@ def time_graph(fn, steps: int) -> float:
     with torch.cuda.graph(g):
         fn()
     return time_region(g.replay, steps, 1) / steps
+
+
+DECODE_STEP_MARKER = "quantize_act_rows"  # the kernel launched once before the timed replays
+
+
+def bench_decode_step_linears(pkg, dev, steps: int, layers: int = 32, batch: int = 64) -> dict:
+    """Config 4's int8 (W8A16) linear stack alone, for a kernel trace: a random-init
+    Llama-3-8B-architecture model quantized as the decode-step runner quantizes it (fused q/k/v,
+    o_proj, fused gate/up with its SiLU-mul, down_proj), the 32 layers' projections at M = batch
+    captured in one graph; one eager pass, one warm-up replay, then `steps` replays. A W8A8
+    activation quantization of one row is launched just before, as a marker the trace summary
+    (`--summarize-decode-step`) starts from."""
+    import torch
+
+    from llm_serving_engine_amd.decode_step import DecodeRunner, random_llama
+
+    model = random_llama(layers, seed=4000, device=dev)
+    runner = DecodeRunner(model, batch, 8)
+    runner.quantize("int8")
+    runner.use("int8")
+    calls = runner.linear_calls(batch)
+    nbytes = runner.linear_bytes(batch)
+    marker = torch.zeros(1, 16, dtype=torch.bfloat16, device=dev)
+    pkg.ops.quantize_act_per_token(marker)
+    t = time_graph(lambda: [mod(x) for mod, x in calls], steps)
+    return {"layers": layers, "batch": batch, "replays": steps,
+            "int8_linear_us_per_step": round(t * 1e6, 1),
+            "int8_linear_gbps": round(nbytes / t / 1e9, 1), "int8_linear_bytes": nbytes}
 
 
 def bench_decode_step(pkg, dev, steps: int, layers: int = 32, batch: int = 64,
@@ -1340,6 +1448,9 @@ def main() -> None:
     if args.summarize_prefill:
         summarize_prefill(*args.summarize_prefill)
         return
+    if args.summarize_decode_step:
+        summarize_decode_step(args.summarize_decode_step)
+        return
     if args.summarize_w8a8:
         summarize_w8a8(*args.summarize_w8a8)
         return
@@ -1387,6 +1498,10 @@ def main() -> None:
         return
     if args.only == "decode-step":
         print(json.dumps({"decode_step": bench_decode_step(pkg, dev, args.steps)}))
+        return
+    if args.only == "decode-step-linears":
+        print(json.dumps({"decode_step_linears": bench_decode_step_linears(pkg, dev,
+                                                                           args.steps)}))
         return
     if args.only == "mid":
         print(json.dumps({"mid_range": bench_mid_range(pkg, dev, args.steps, gen)}))
