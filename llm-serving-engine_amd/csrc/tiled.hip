@@ -97,7 +97,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
 tiled_gemm_kernel(TiledArgs a) {
   using Acc = std::conditional_t<I8, i32x4, f32x4>;
   static_assert(!BFW || (!I8 && !GLU), "bf16 weights: plain W16A16 only");
-  static_assert(!STAGE_Y || (!I8 && !GLU && !BFW), "staged output: plain W8A16 only");
+  static_assert(!STAGE_Y || (!GLU && !BFW && (!I8 || (BM == 256 && BN == 256 && WGM == 2))),
+                "staged output: plain W8A16, or the W8A8 256 x 256 tile");
   constexpr int W = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -122,6 +123,12 @@ tiled_gemm_kernel(TiledArgs a) {
   // 1-8 % faster for the 256 x 256 tile and up to 8 % for 64 x 128 at M = 512; with two wave
   // rows (2 x 4) it measured 3-5 % slower, so those keep the plain schedule.
   constexpr bool WAHEAD = !I8 && !BFW && WGM == 1;
+  // W8A8 256 x 256 (2 x 4 waves of 128 x 64, 32 MFMAs per wave and stage): the two wave rows
+  // run the K loop half a stage apart (ping-pong, below). On MI355X at M = 512..4096 over the
+  // Llama-3-8B shapes 3-12 % faster than the common schedule, bit-identical; on the 128 x 256,
+  // 256 x 128 and 128 x 128 tiles (16 or 8 MFMAs per wave and stage, shorter than a wave's
+  // reads and DMA issue) 2-20 % slower, so they keep the common schedule.
+  constexpr bool PING = I8 && BM == 256 && BN == 256 && WGM == 2 && WGN == 4 && !NT;
 
   // One LDS array per stage slot (x image, then the weight tiles and their padding); with
   // STAGE_Y one array of all NST slots, which the epilogue reuses for the block's output tile.
@@ -341,6 +348,59 @@ tiled_gemm_kernel(TiledArgs a) {
       }
     };
     run_steps(step);
+  } else if constexpr (PING) {
+    // Ping-pong: the wave rows alternate. Each SIMD holds one wave of each row; while row 0
+    // issues its stage's 32 MFMAs, row 1 issues its DMA share and reads its fragments, then they
+    // swap, so the matrix core sees one wave's MFMA run after the other's instead of both waves
+    // stalling on LDS reads and the barrier together. Row 1 starts one barrier late; every wave
+    // then passes two barriers per stage (after its reads, after its MFMAs) and row 0 one more at
+    // the end, so both rows pass the same count. With barrier c separating phases, slot kt % NST
+    // is read by row 0 in the phase before row 1 reads it, and the DMA that overwrites it
+    // (stage kt + NST, issued at the top of stage kt + 1) comes after both. A wave's stage kt + 1
+    // loads must have landed before the barrier that opens row 0's reads of it: row 0 waits
+    // after its MFMAs of stage kt, row 1 after its reads of stage kt (the end of the same phase).
+    const bool row1 = wm == 1;
+#pragma unroll
+    for (int i = 0; i < NST - 1; ++i) {
+      load_x(i, i);
+      load_w(i, i);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+    __builtin_amdgcn_s_barrier();
+    if (row1) __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    auto step = [&](int kt, int i, bool live) {
+      load_x(kt + NST - 1, (i + NST - 1) % NST);
+      load_w(kt + NST - 1, (i + NST - 1) % NST);
+      const uint4* xs = xslot(i);
+      const uint4* ws = wslot(i) + 64 * wn * TN + lane;
+      uint4 wv[TN], xv[TM];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) wv[j] = ws[64 * j];
+#pragma unroll
+      for (int ii = 0; ii < TM; ++ii) {
+        const int r = wm * WM + 16 * ii + r16;
+        xv[ii] = xs[r * XCH + (g ^ tiled_swz<I8>(r))];
+      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(63));
+      if (row1) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+      // The fences keep the compiler from moving MFMAs or reads across the phase barriers.
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (live) {
+#pragma unroll
+        for (int ii = 0; ii < TM; ++ii)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[ii][j] = mfma_i8(wv[j], xv[ii], acc[ii][j]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (!row1) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    run_steps(step);
+    if (!row1) __builtin_amdgcn_s_barrier();
   } else {
     // Prologue: stages 0 .. NST-2 in flight.
 #pragma unroll
@@ -406,7 +466,51 @@ tiled_gemm_kernel(TiledArgs a) {
     }
     return;
   }
-  if constexpr (STAGE_Y) {
+  if constexpr (STAGE_Y && I8) {
+    // W8A8 (no int32 output): each wave's 128 x 64 bf16 tile goes through its own 16 KB of the
+    // ring (rows of 128 bytes whose 16-byte chunks are XOR-swizzled by row) and out as whole
+    // 128-byte row segments, 8 rows per store, with the nontemporal policy; the direct stores
+    // below write 32-byte pieces of 16 rows each. Same values. On MI355X over launches of more
+    // than one round of blocks 3-11 % faster (gate_up at M = 2048 / 4096: 253 -> 229 /
+    // 457 -> 408 us); with one round up to 8 % slower, so the host picks it for longer launches.
+    static_assert(WN == 64 && W * WM * WN * 2 <= NST * SLOT * 16, "per-wave staging fits the ring");
+    if (a.y && (a.ldy & 7) == 0 && ((uintptr_t)a.y & 15) == 0 && !a.acc) {
+      __syncthreads();  // every wave's reads of the ring have completed (loads drained above)
+      char* ys = reinterpret_cast<char*>(st0 + wave * (WM * 128 / 16));
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = 16 * i + r16, m = m0 + wm * WM + row;
+        const float sxm = m < a.M ? a.sx[m] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = n0 + wn * WN + 16 * j + 4 * g;
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            o[r] = scaled<I8>(acc[i][j], r, n + r < a.N ? a.s[n + r] : 0.0f, sxm);
+          const int chunk = (2 * j + (g >> 1)) ^ (row & 7);
+          *reinterpret_cast<uint2*>(ys + row * 128 + chunk * 16 + 8 * (g & 1)) =
+              make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+        }
+      }
+      // A wave's LDS accesses complete in order, so its reads below see its writes above.
+#pragma unroll
+      for (int k = 0; k < WM / 8; ++k) {
+        const int row = 8 * k + (lane >> 3), c = lane & 7;
+        const int m = m0 + wm * WM + row, n = n0 + wn * WN + 8 * c;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ys + row * 128 + ((c ^ (row & 7)) * 16));
+        if (m >= a.M || n >= a.N) continue;
+        uint16_t* out = a.y + (int64_t)m * a.ldy + n;
+        if (n + 8 <= a.N) {
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out));
+        } else {
+          const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+          for (int t = 0; t < a.N - n; ++t) out[t] = e[t];
+        }
+      }
+      return;
+    }
+  } else if constexpr (STAGE_Y) {
     // The block's bf16 tile goes through LDS (rows padded by 16 bytes, which spreads the
     // 16-row column writes over the banks) and out as whole rows of 16-byte stores. Same values
     // as the direct stores below, which remain for a y not 16-byte aligned row by row.
@@ -479,8 +583,9 @@ static const void* tiled_fn() {
   // 256 x 256 and 9-12 % for 128 x 256 (it reads twice the x fragments, which the conflict-free
   // swizzle and LDS's 256 bytes per clock of b128 reads absorb). In W8A8 (no dequantization)
   // 2 x 4 stays faster. Stage slots: 3 for bf16 x (4 would not fit the 256 x 256 tile, and
-  // measured no faster on the others), 4 for int8 x except the 256 x 256 tile (3: 1-7 % faster).
-  constexpr int nst = (I8 && !(BM == 256 && BN == 256)) ? 4 : 3;
+  // measured no faster on the others), 4 for int8 x (with the 256 x 256 tile's ping-pong schedule
+  // 1-2 % faster than 3).
+  constexpr int nst = I8 ? 4 : 3;
   constexpr int wgm = (!I8 && BN == 256) ? 1 : 2;
   static_assert(64 * wgm * (8 / wgm) == kTiledThreads, "8 waves");
   return reinterpret_cast<const void*>(
@@ -499,7 +604,9 @@ static const void* tiled_fn() {
 // activations) W8A8 gate_up 2-4 % faster and W8A16 unchanged. With two block rows (M > 128) nt
 // measured 8-14 % slower.
 //
-// `stage_y`: a W8A16 256 x 256 launch (no gate/up) of at least kStageYRounds rounds of blocks,
+// `stage_y`, W8A8: a 256 x 256 launch (no gate/up, no int32 output) of more than one round of
+// blocks, whose waves write their output tiles through LDS (STAGE_Y with I8).
+// `stage_y`, W8A16: a 256 x 256 launch (no gate/up) of at least kStageYRounds rounds of blocks,
 // whose output tiles go out through LDS as whole rows (STAGE_Y). Measured on MI355X against the
 // direct stores, bit-identical: q/k/v at M = 8192 (3 rounds) 319 -> 311 us, gate_up at 8192 (14
 // rounds) 1460 -> 1425 us, at 2048 (3.5 rounds) 410 -> 397 us; with one or two rounds unchanged
@@ -545,6 +652,10 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
       if (stage_y)
         return reinterpret_cast<const void*>(
             &tiled_gemm_kernel<false, 256, 256, 1, 8, 3, false, false, false, true>);
+    } else if constexpr (I8 && !GLU) {
+      if (stage_y)
+        return reinterpret_cast<const void*>(
+            &tiled_gemm_kernel<true, 256, 256, 2, 4, 4, false, false, false, true>);
     }
     return tiled_fn<I8, 256, 256, GLU>();
   }
@@ -652,8 +763,10 @@ static int launch_tiled_range(const TiledShape& sh, bool decode, const void* x, 
   if (blocks > 0x7fffffff) return LSE_E_RANGE;
   void* args[] = {&a};
   const bool one_row = a.mblocks == 1;
-  const bool stage_y = !I8 && glu == 0 && !decode && sh.bm == 256 && sh.bn == 256 &&
-                       blocks >= (int64_t)kStageYRounds * device_cus();
+  const bool stage_y =
+      glu == 0 && !decode && sh.bm == 256 && sh.bn == 256 &&
+      (I8 ? !acc && blocks > (int64_t)device_cus()
+          : blocks >= (int64_t)kStageYRounds * device_cus());
   const void* fn = glu > 0 ? tiled_kernel_for<I8, true>(sh, decode, one_row)
                             : tiled_kernel_for<I8, false>(sh, decode, one_row, stage_y);
   if (!fn) return LSE_E_RANGE;

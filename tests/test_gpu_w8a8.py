@@ -259,3 +259,32 @@ def test_one_launch_route_at_llama_shapes(pkg, dev, k, n):
         np.testing.assert_array_equal(bf16_bits(y), y_ref, err_msg=f"one-launch y M={m}")
         y2, acc2 = pkg.ops.w8a8_gemm(xq2, sx2, qp, s, True)
         assert torch.equal(acc, acc2) and torch.equal(y, y2), f"routes differ at M={m}"
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 28672, 4096), (2048, 28672, 4096), (1500, 20000, 1024),
+                                   (1500, 20004, 1024), (3000, 8200, 512)])
+def test_staged_output_tiles_match_the_oracle(pkg, dev, m, n, k):
+    """W8A8 launches of more than one round of 256 x 256 blocks without an int32 output write
+    their bf16 tiles through LDS as whole row segments (gate_up at 4096 tokens: one launch of 7
+    rounds; at 2048: the 3-round bulk launch); with the int32 output requested the kernels store
+    directly. Both outputs bit-identical, and equal to the oracle's epilogue of the exact
+    accumulators (checked against an fp64 GEMM on the GPU). Ragged M and N (partial edge tiles:
+    1500 x 20000 and 3000 x 8200 in one launch of 474 and 396 blocks), and a row length not a
+    multiple of 8 (20004), where the kernel keeps its direct stores."""
+    x_bits, w = ora.seeded_inputs(7100 + m + n + k, m, n, k, outliers=True)
+    q, s = pkg.ops.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    del w
+    qp = pkg.ops.pack_weight(q)
+    xq, sx = pkg.ops.quantize_act_per_token(to_bf16_tensor(x_bits, dev))
+    y_staged, none_acc = pkg.ops.w8a8_gemm(xq, sx, qp, s, want_acc=False, want_y=True)
+    y_direct, acc = pkg.ops.w8a8_gemm(xq, sx, qp, s, want_acc=True, want_y=True)
+    assert none_acc is None
+    assert torch.equal(y_staged, y_direct), f"M={m} N={n} K={k}"
+    exact = (xq.double() @ q.double().t()).round().to(torch.int64)
+    assert torch.equal(acc.to(torch.int64), exact), f"M={m} N={n} K={k}"
+    del exact
+    s_host, sx_host = s.cpu().numpy(), sx.cpu().numpy()
+    for r0 in range(0, m, 1024):
+        y_ref = ora.w8a8_epilogue(acc[r0:r0 + 1024].cpu().numpy(), sx_host[r0:r0 + 1024], s_host)
+        np.testing.assert_array_equal(bf16_bits(y_staged[r0:r0 + 1024]), y_ref,
+                                      err_msg=f"rows {r0}..")
