@@ -659,7 +659,12 @@ static SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K, bool glu = fals
                                 bool nosplit = false) {
   if (M <= 16) {
     const bool fits = M * (size_t)skinny_x_row((int)K, I8 ? 1 : 2) <= (size_t)kSkinnyXLdsBytes;
-    return {1, glu ? 2 : 1, 8, 4, fits, 1};
+    // A weight ring of 2 when every wave has at most one K step (K <= 512): the 4-deep ring
+    // would run three padding steps whose out-of-range loads still cross the memory pipeline.
+    // On MI355X the trivial call (M 1, K 64, N 16) 3.82 -> 3.43 us per graph-replayed launch.
+    // The ring depth changes no summation order (padding steps add zero products).
+    const int dw = !glu && fits && ceil_div(ceil_div(K, kTileK), 8) <= 1 ? 2 : 4;
+    return {1, glu ? 2 : 1, 8, dw, fits, 1};
   }
   const int mt = M <= 32 ? 2 : 4;
   if (!glu && !nosplit && skinny_split_k(N, K)) return {mt, 4, 4, 4, false, 4};
@@ -686,9 +691,11 @@ static const void* skinny_kernel_for(const SkinnyShape& sh) {
       return sh.xlds ? skinny_fn<I8, 1, 2, 8, 4, 1, true, true>()
                      : skinny_fn<I8, 1, 2, 8, 4, 4, false, true>();
   } else {
-    if (sh.mt == 1)
+    if (sh.mt == 1) {
+      if (sh.dw == 2) return skinny_fn<I8, 1, 1, 8, 2, 1, true, false, BFW>();  // xlds
       return sh.xlds ? skinny_fn<I8, 1, 1, 8, 4, 1, true, false, BFW>()
                      : skinny_fn<I8, 1, 1, 8, 4, 4, false, false, BFW>();
+    }
     if (sh.rt == 1) {
       if (sh.mt == 2)
         return sh.w == 4 ? skinny_fn<I8, 2, 1, 4, 4, 4, false, false, BFW>()
@@ -926,7 +933,10 @@ int launch_w8a8_skinny_quantizing(const uint16_t* x, int64_t ldx, const int8_t* 
   const SkinnyShape sh = skinny_shape<true>(M, N, K);
   if (sh.mt != 1 || !sh.xlds || sh.splits != 1) return LSE_E_ALGO;
   SkinnyPlan pl = skinny_plan_for<true>(
-      sh, skinny_fn<true, 1, 1, 8, 4, 1, true, false, false, true>(), M, N, K);
+      sh,
+      sh.dw == 2 ? skinny_fn<true, 1, 1, 8, 2, 1, true, false, false, true>()
+                 : skinny_fn<true, 1, 1, 8, 4, 1, true, false, false, true>(),
+      M, N, K);
   SkinnyArgs& a = pl.a;
   a.x = x;
   a.ldx = ldx;
