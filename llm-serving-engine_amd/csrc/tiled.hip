@@ -124,10 +124,12 @@ tiled_gemm_kernel(TiledArgs a) {
   // rows (2 x 4) it measured 3-5 % slower, so those keep the plain schedule.
   constexpr bool WAHEAD = !I8 && !BFW && WGM == 1;
   // W8A8 256 x 256 (2 x 4 waves of 128 x 64, 32 MFMAs per wave and stage): the two wave rows
-  // run the K loop half a stage apart (ping-pong, below). On MI355X at M = 512..4096 over the
-  // Llama-3-8B shapes 3-12 % faster than the common schedule, bit-identical; on the 128 x 256,
-  // 256 x 128 and 128 x 128 tiles (16 or 8 MFMAs per wave and stage, shorter than a wave's
-  // reads and DMA issue) 2-20 % slower, so they keep the common schedule.
+  // run the K loop half a pair of stages apart (ping-pong, below). On MI355X at M = 512..4096
+  // over the Llama-3-8B shapes 3-12 % faster than the common schedule with one stage per phase,
+  // bit-identical, and two stages per phase another 1-3 % (ten of ten cases, alternated); on
+  // the 128 x 256, 256 x 128 and 128 x 128 tiles (16 or 8 MFMAs per wave and stage, shorter than
+  // a wave's reads and DMA issue) ping-pong measured 2-20 % slower, so they keep the common
+  // schedule.
   constexpr bool PING = I8 && BM == 256 && BN == 256 && WGM == 2 && WGN == 4 && !NT;
 
   // One LDS array per stage slot (x image, then the weight tiles and their padding); with
@@ -350,56 +352,88 @@ tiled_gemm_kernel(TiledArgs a) {
     run_steps(step);
   } else if constexpr (PING) {
     // Ping-pong: the wave rows alternate. Each SIMD holds one wave of each row; while row 0
-    // issues its stage's 32 MFMAs, row 1 issues its DMA share and reads its fragments, then they
-    // swap, so the matrix core sees one wave's MFMA run after the other's instead of both waves
-    // stalling on LDS reads and the barrier together. Row 1 starts one barrier late; every wave
-    // then passes two barriers per stage (after its reads, after its MFMAs) and row 0 one more at
-    // the end, so both rows pass the same count. With barrier c separating phases, slot kt % NST
-    // is read by row 0 in the phase before row 1 reads it, and the DMA that overwrites it
-    // (stage kt + NST, issued at the top of stage kt + 1) comes after both. A wave's stage kt + 1
-    // loads must have landed before the barrier that opens row 0's reads of it: row 0 waits
-    // after its MFMAs of stage kt, row 1 after its reads of stage kt (the end of the same phase).
+    // issues its 64 MFMAs of a pair of K stages, row 1 reads its fragments of that pair (and the
+    // reverse a phase later), so the matrix core sees one wave's MFMA run after the other's
+    // instead of both waves stalling on LDS reads and the barrier together. Pair q is stages
+    // 2q, 2q+1 in slots 2(q & 1), 2(q & 1) + 1. Row 1 starts one barrier late; every wave then
+    // passes two barriers per pair (after its reads, after its MFMAs) and row 0 one more at the
+    // end, so both rows pass the same count. Phases (c = barrier count): row 0 reads pair q while
+    // row 1 multiplies pair q - 1, then row 0 multiplies pair q while row 1 reads it.
+    //  * Row 0 issues its DMA share of pair q + 1 at the top of its reading phase of pair q, into
+    //    the slots of pair q - 1, which row 1 finished reading at the barrier that opened the
+    //    phase; it waits for that DMA (vmcnt 0) after its MFMAs of pair q, before the barrier
+    //    that opens its reads of pair q + 1.
+    //  * Row 1 issues its share of pair q + 2 at the end of its reading phase of pair q, into the
+    //    slots of pair q, which row 0 read in the phase before; its wait there (all but that
+    //    pair) lands its share of pair q + 1 before the same barrier.
+    static_assert(NST == 4, "ping-pong: two pairs of stage slots");
     const bool row1 = wm == 1;
-#pragma unroll
-    for (int i = 0; i < NST - 1; ++i) {
-      load_x(i, i);
-      load_w(i, i);
-    }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+    load_x(0, 0);
+    load_w(0, 0);
+    load_x(1, 1);
+    load_w(1, 1);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
-    if (row1) __builtin_amdgcn_s_barrier();
+    if (row1) {
+      load_x(2, 2);
+      load_w(2, 2);
+      load_x(3, 3);
+      load_w(3, 3);
+      __builtin_amdgcn_s_barrier();
+    }
     __builtin_amdgcn_sched_barrier(0);
-    auto step = [&](int kt, int i, bool live) {
-      load_x(kt + NST - 1, (i + NST - 1) % NST);
-      load_w(kt + NST - 1, (i + NST - 1) % NST);
-      const uint4* xs = xslot(i);
-      const uint4* ws = wslot(i) + 64 * wn * TN + lane;
-      uint4 wv[TN], xv[TM];
+    auto pair = [&](int q, auto slot_pair, bool live0, bool live1) {
+      constexpr int sb = 2 * decltype(slot_pair)::value;  // slots of pair q
+      constexpr int so = 2 - sb;                          // slots of pairs q - 1 and q + 1
+      if (!row1) {
+        load_x(2 * q + 2, so);
+        load_w(2 * q + 2, so);
+        load_x(2 * q + 3, so + 1);
+        load_w(2 * q + 3, so + 1);
+      }
+      uint4 wv[2][TN], xv[2][TM];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) wv[j] = ws[64 * j];
+      for (int h = 0; h < 2; ++h) {
+        const uint4* xs = xslot(sb + h);
+        const uint4* ws = wslot(sb + h) + 64 * wn * TN + lane;
 #pragma unroll
-      for (int ii = 0; ii < TM; ++ii) {
-        const int r = wm * WM + 16 * ii + r16;
-        xv[ii] = xs[r * XCH + (g ^ tiled_swz<I8>(r))];
+        for (int j = 0; j < TN; ++j) wv[h][j] = ws[64 * j];
+#pragma unroll
+        for (int ii = 0; ii < TM; ++ii) {
+          const int r = wm * WM + 16 * ii + r16;
+          xv[h][ii] = xs[r * XCH + (g ^ tiled_swz<I8>(r))];
+        }
       }
       __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(63));
-      if (row1) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+      if (row1) {
+        load_x(2 * q + 4, sb);
+        load_w(2 * q + 4, sb);
+        load_x(2 * q + 5, sb + 1);
+        load_w(2 * q + 5, sb + 1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LOADS));
+      }
       // The fences keep the compiler from moving MFMAs or reads across the phase barriers.
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      if (live) {
 #pragma unroll
-        for (int ii = 0; ii < TM; ++ii)
+      for (int h = 0; h < 2; ++h) {
+        if (h == 0 ? live0 : live1) {
 #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[ii][j] = mfma_i8(wv[j], xv[ii], acc[ii][j]);
+          for (int ii = 0; ii < TM; ++ii)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[ii][j] = mfma_i8(wv[h][j], xv[h][ii], acc[ii][j]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (!row1) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+      if (!row1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     };
-    run_steps(step);
+    for (int q0 = 0; 2 * q0 < nloc; q0 += 2) {
+      pair(q0, std::integral_constant<int, 0>{}, 2 * q0 < nloc, 2 * q0 + 1 < nloc);
+      pair(q0 + 1, std::integral_constant<int, 1>{}, 2 * q0 + 2 < nloc, 2 * q0 + 3 < nloc);
+    }
     if (!row1) __builtin_amdgcn_s_barrier();
   } else {
     // Prologue: stages 0 .. NST-2 in flight.
