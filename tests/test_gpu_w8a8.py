@@ -288,3 +288,25 @@ def test_staged_output_tiles_match_the_oracle(pkg, dev, m, n, k):
         y_ref = ora.w8a8_epilogue(acc[r0:r0 + 1024].cpu().numpy(), sx_host[r0:r0 + 1024], s_host)
         np.testing.assert_array_equal(bf16_bits(y_staged[r0:r0 + 1024]), y_ref,
                                       err_msg=f"rows {r0}..")
+
+
+@pytest.mark.parametrize("k", [64, 80, 1040])
+def test_ping_pong_tile_with_odd_and_single_k_steps(pkg, dev, k):
+    """The W8A8 256 x 256 tile runs its K loop in pairs of stages: one K step (64), two with a
+    partial last one (80) and an odd count (1040: 17 steps) leave the last pair half or wholly
+    empty. 1500 x 20000 takes that tile in one launch of 474 blocks (ragged in M and N), staged
+    output without the int32 result, direct stores with it: accumulators exact against an fp64
+    GEMM on the GPU, both outputs equal to the oracle's epilogue."""
+    m, n = 1500, 20000
+    x_bits, w = ora.seeded_inputs(7300 + k, m, n, k, outliers=True)
+    q, s = pkg.ops.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    del w
+    qp = pkg.ops.pack_weight(q)
+    xq, sx = pkg.ops.quantize_act_per_token(to_bf16_tensor(x_bits, dev))
+    y_staged, _ = pkg.ops.w8a8_gemm(xq, sx, qp, s, want_acc=False, want_y=True)
+    y_direct, acc = pkg.ops.w8a8_gemm(xq, sx, qp, s, want_acc=True, want_y=True)
+    exact = (xq.double() @ q.double().t()).round().to(torch.int64)
+    assert torch.equal(acc.to(torch.int64), exact), f"K={k}"
+    assert torch.equal(y_staged, y_direct), f"K={k}"
+    y_ref = ora.w8a8_epilogue(acc.cpu().numpy(), sx.cpu().numpy(), s.cpu().numpy())
+    np.testing.assert_array_equal(bf16_bits(y_direct), y_ref)
