@@ -169,6 +169,38 @@ tiled_gemm_kernel(TiledArgs a) {
   const int bm = first_bm + tg % gm, bn = tg / gm;
   const int m0 = bm * BM, n0 = bn * BN, rb0 = n0 / 16;
 
+  // The scales the block's epilogue applies, staged in LDS by direct-to-LDS loads issued before
+  // the stage prologue (every later wait covers them): per-channel scales of its BN output rows
+  // (gate/up: gate and up scales of its BN / 2 output columns) and in W8A8 the per-token scales
+  // of its BM rows; a 1 KB load each, zeros past N and M. Read from global memory after the last
+  // MFMA they were a string of dependent small loads: on MI355X the W8A8 256 x 256 tile took
+  // 447 against 497 us for gate_up at M = 4096 (70 against 77 at 512), o_proj 70 against 77,
+  // down_proj 202 against 212; the other tiles 0-4 % less. Same values.
+  // (Not the 96-row tile: it fills exactly half the LDS, two blocks per CU, and reads its scales
+  // from global memory.)
+  constexpr bool SCL = !BFW && BM != 96;
+  constexpr int SC_UP = 256, SC_X = GLU ? 512 : 256;
+  __shared__ float sc_lds[SCL ? SC_X + (I8 ? 256 : 0) : 1];
+  // Scale of output row (column) n / gate and up scales of output column n / token scale of m.
+  auto scale_n = [&](int n) { return SCL ? sc_lds[n - n0] : a.s[n]; };
+  auto scale_gate = [&](int n) { return SCL ? sc_lds[n - 16 * (rb0 >> 1)] : a.s[n]; };
+  auto scale_up = [&](int n) {
+    return SCL ? sc_lds[SC_UP + n - 16 * (rb0 >> 1)] : a.s[a.glu_up + n];
+  };
+  auto scale_m = [&](int m) { return SCL ? sc_lds[SC_X + m - m0] : a.sx[m]; };
+  if constexpr (SCL) {
+    if (S == 1) {
+      const int c0 = GLU ? 16 * (rb0 >> 1) : n0;  // first output column (gate/up: of the gate half)
+      const int ncols = GLU ? a.glu : a.N;
+      const uint32_t cbytes = (uint32_t)max(0, ncols - c0) * 4u;
+      if (wave == 0) dma16_lds<0>(make_rsrc4(a.s + c0, cbytes), lds_addr(sc_lds), 16u * lane);
+      if (GLU && wave == 1)
+        dma16_lds<0>(make_rsrc4(a.s + a.glu_up + c0, cbytes), lds_addr(sc_lds + SC_UP), 16u * lane);
+      if (I8 && wave == 2)
+        dma16_lds<0>(make_rsrc4(a.sx + m0, (uint32_t)max(0, a.M - m0) * 4u), lds_addr(sc_lds + SC_X),
+                     16u * lane);
+    }
+  }
   // Buffer resources based at the block's first row / row tile, so 32-bit offsets suffice.
   const int rows = min(BM, a.M - m0);
   const u32x4 xres = make_rsrc4(static_cast<const char*>(a.x) + (int64_t)m0 * a.ldx * ESZ,
@@ -483,7 +515,7 @@ tiled_gemm_kernel(TiledArgs a) {
     for (int i = 0; i < TM; ++i) {
       const int m = m0 + wm * WM + 16 * i + r16;
       if (m >= a.M) continue;
-      const float sxm = I8 ? a.sx[m] : 0.0f;
+      const float sxm = I8 ? scale_m(m) : 0.0f;
 #pragma unroll
       for (int j = 0; j < TN; j += 2) {
         const int n = 16 * ((rb0 + wn * TN + j) >> 1) + 4 * g;
@@ -492,8 +524,8 @@ tiled_gemm_kernel(TiledArgs a) {
         float sg[4], su[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          sg[r] = r < cnt ? a.s[n + r] : 0.0f;
-          su[r] = r < cnt ? a.s[a.glu_up + n + r] : 0.0f;
+          sg[r] = r < cnt ? scale_gate(n + r) : 0.0f;
+          su[r] = r < cnt ? scale_up(n + r) : 0.0f;
         }
         store_glu4<I8>(a.y, a.ldy, m, n, cnt, acc[i][j], acc[i][j + 1], sg, su, sxm, yvec);
       }
@@ -514,14 +546,14 @@ tiled_gemm_kernel(TiledArgs a) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = 16 * i + r16, m = m0 + wm * WM + row;
-        const float sxm = m < a.M ? a.sx[m] : 0.0f;
+        const float sxm = m < a.M ? scale_m(m) : 0.0f;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int n = n0 + wn * WN + 16 * j + 4 * g;
           float o[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            o[r] = scaled<I8>(acc[i][j], r, n + r < a.N ? a.s[n + r] : 0.0f, sxm);
+            o[r] = scaled<I8>(acc[i][j], r, n + r < a.N ? scale_n(n + r) : 0.0f, sxm);
           const int chunk = (2 * j + (g >> 1)) ^ (row & 7);
           *reinterpret_cast<uint2*>(ys + row * 128 + chunk * 16 + 8 * (g & 1)) =
               make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
@@ -562,7 +594,7 @@ tiled_gemm_kernel(TiledArgs a) {
           float o[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            o[r] = scaled<false>(acc[i][j], r, n + r < a.N ? a.s[n + r] : 0.0f, 0.0f);
+            o[r] = scaled<false>(acc[i][j], r, n + r < a.N ? scale_n(n + r) : 0.0f, 0.0f);
           *reinterpret_cast<uint2*>(ys + ml * YROW + nl * 2) =
               make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
         }
@@ -589,7 +621,7 @@ tiled_gemm_kernel(TiledArgs a) {
   for (int i = 0; i < TM; ++i) {
     const int m = m0 + wm * WM + 16 * i + r16;
     if (m >= a.M) continue;
-    const float sxm = I8 ? a.sx[m] : 0.0f;
+    const float sxm = I8 ? scale_m(m) : 0.0f;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + wn * WN + 16 * j + 4 * g;
@@ -597,7 +629,7 @@ tiled_gemm_kernel(TiledArgs a) {
       const int cnt = min(4, a.N - n);
       float sc[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = BFW ? 1.0f : r < cnt ? a.s[n + r] : 0.0f;
+      for (int r = 0; r < 4; ++r) sc[r] = BFW ? 1.0f : r < cnt ? scale_n(n + r) : 0.0f;
       store_out4<I8>(a.y, a.ldy, a.acc, a.N, m, n, cnt, acc[i][j], sc, sxm, yvec);
     }
   }
