@@ -391,26 +391,58 @@ tiled_gemm_kernel(TiledArgs a) {
     // passes two barriers per pair (after its reads, after its MFMAs) and row 0 one more at the
     // end, so both rows pass the same count. Phases (c = barrier count): row 0 reads pair q while
     // row 1 multiplies pair q - 1, then row 0 multiplies pair q while row 1 reads it.
-    //  * Row 0 issues its DMA share of pair q + 1 at the top of its reading phase of pair q, into
-    //    the slots of pair q - 1, which row 1 finished reading at the barrier that opened the
-    //    phase; it waits for that DMA (vmcnt 0) after its MFMAs of pair q, before the barrier
-    //    that opens its reads of pair q + 1.
-    //  * Row 1 issues its share of pair q + 2 at the end of its reading phase of pair q, into the
-    //    slots of pair q, which row 0 read in the phase before; its wait there (all but that
-    //    pair) lands its share of pair q + 1 before the same barrier.
-    static_assert(NST == 4, "ping-pong: two pairs of stage slots");
+    //  * The loads split by wave row, so that no wave's DMA can overwrite LDS another wave of its
+    //    row still reads: row 0 fills the x image (wave w: 1 KB pieces w + 4 i, i < 4), each
+    //    row-1 wave the four weight tiles its wave column reads, which only it and the row-0
+    //    wave of that column read. (Split as in the common schedule, a row-1 wave's DMA raced
+    //    the other row-1 waves' fragment reads of the x rows it had loaded; seen only when the
+    //    DMA read past K, whose zeros land at once.)
+    //  * Row 0 issues x of pair q + 1 at the top of its reading phase of pair q, into the slots
+    //    of pair q - 1, which row 1 finished reading at the barrier that opened the phase; it
+    //    waits for that DMA (vmcnt 0) after its MFMAs of pair q, before the barrier that opens
+    //    its reads of pair q + 1.
+    //  * Row 1 issues the weights of pair q + 2 at the end of its reading phase of pair q, into
+    //    the slots of pair q, which the row-0 wave of its column read in the phase before; its
+    //    wait there (all but that pair) lands the weights of pair q + 1 before the same barrier.
+    static_assert(NST == 4 && XI + WI == 4 && TN == 4 && XBYTES == 4 * 4096 && WH == 1,
+                  "ping-pong: two pairs of slots, four 1 KB loads per wave and stage");
     const bool row1 = wm == 1;
-    load_x(0, 0);
-    load_w(0, 0);
-    load_x(1, 1);
-    load_w(1, 1);
+    const uint32_t x_step4 = (uint32_t)(4 * RPL) * (uint32_t)a.ldx;
+    auto load_x4 = [&](int kt, int slot) {
+      kt += kbeg;
+      const bool kv = kt < kend && XROW * kt + x_kb < a.K;
+      uint32_t xo[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xo[i] = kv && x_r0 + 4 * RPL * i < rows ? x_base + i * x_step4 + XROW * kt : kOutOfRange;
+      dma16_lds_seq<4096>(xres, x_lds[slot], xo, std::make_integer_sequence<int, 4>{});
+    };
+    auto load_w4 = [&](int kt, int slot) {
+      kt += kbeg;
+      uint32_t wo[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tile = TN * wn + i;
+        wo[i] = kt < kend && tile < rtiles
+                    ? ((uint32_t)tile * (uint32_t)a.nsteps + (uint32_t)kt) * kTileBytes + 16u * lane
+                    : kOutOfRange;
+      }
+      dma16_lds_seq<1024>(qres, lds_addr(wslot(slot) + 64 * TN * wn), wo,
+                          std::make_integer_sequence<int, 4>{});
+    };
+    auto load4 = [&](int kt, int slot) {
+      if (row1)
+        load_w4(kt, slot);
+      else
+        load_x4(kt, slot);
+    };
+    load4(0, 0);
+    load4(1, 1);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
     if (row1) {
-      load_x(2, 2);
-      load_w(2, 2);
-      load_x(3, 3);
-      load_w(3, 3);
+      load_w4(2, 2);
+      load_w4(3, 3);
       __builtin_amdgcn_s_barrier();
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -418,10 +450,8 @@ tiled_gemm_kernel(TiledArgs a) {
       constexpr int sb = 2 * decltype(slot_pair)::value;  // slots of pair q
       constexpr int so = 2 - sb;                          // slots of pairs q - 1 and q + 1
       if (!row1) {
-        load_x(2 * q + 2, so);
-        load_w(2 * q + 2, so);
-        load_x(2 * q + 3, so + 1);
-        load_w(2 * q + 3, so + 1);
+        load_x4(2 * q + 2, so);
+        load_x4(2 * q + 3, so + 1);
       }
       uint4 wv[2][TN], xv[2][TM];
 #pragma unroll
@@ -438,11 +468,9 @@ tiled_gemm_kernel(TiledArgs a) {
       }
       __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(63));
       if (row1) {
-        load_x(2 * q + 4, sb);
-        load_w(2 * q + 4, sb);
-        load_x(2 * q + 5, sb + 1);
-        load_w(2 * q + 5, sb + 1);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LOADS));
+        load_w4(2 * q + 4, sb);
+        load_w4(2 * q + 5, sb + 1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
       }
       // The fences keep the compiler from moving MFMAs or reads across the phase barriers.
       __builtin_amdgcn_sched_barrier(0);
@@ -488,7 +516,8 @@ tiled_gemm_kernel(TiledArgs a) {
     run_steps(step);
   }
 
-  // The last stages' loads (past K, so they moved no data) are drained before the epilogue.
+  // The last stages' loads (past K: they write zeros into their slots) are drained before the
+  // epilogue.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // Epilogue. D tile (i, j): lane holds weight rows 4 g + r (r = 0..3) of token r16.
