@@ -788,7 +788,11 @@ constexpr TiledShape kTileCand[kTileCands] = {{256, 256}, {256, 128}, {128, 256}
                                               {64, 128},  {256, 192}, {96, 128}};
 constexpr double kTileEff16[kTileCands] = {1.0, 0.86, 0.87, 0.835, 0.6, 0.92, 0.75};
 // (256 x 192 and 96 x 128 serve W8A16 only.)
-constexpr double kTileEff8[kTileCands] = {1.0, 0.81, 0.865, 0.86, 0.6, 0.926, 0.75};
+// W8A8 re-measured once its 256 x 256 tile ran ping-pong with LDS-staged scales (averages over
+// the four shapes at M = 8192: 256 x 128 0.76, 128 x 256 0.80, 128 x 128 0.72); the picks that
+// changed (gate_up at M = 384, q/k/v at 2048, o_proj and down_proj at 3072: 256 x 256 instead of
+// 128 x 128) measured 11-19 % faster.
+constexpr double kTileEff8[kTileCands] = {1.0, 0.76, 0.80, 0.72, 0.6, 0.926, 0.75};
 
 // One round of candidate i on every CU, in the cost model's units.
 template <bool I8>
