@@ -131,6 +131,9 @@ tiled_gemm_kernel(TiledArgs a) {
   // a wave's reads and DMA issue) ping-pong measured 2-20 % slower, so they keep the common
   // schedule.
   constexpr bool PING = I8 && BM == 256 && BN == 256 && WGM == 2 && WGN == 4 && !NT;
+  // W8A16 256 x 256 (2 x 4 waves of 128 x 64, 64 MFMAs per wave and stage): the same two wave
+  // rows half a stage apart, one stage per phase (PW, below).
+  constexpr bool PW = !I8 && !BFW && BM == 256 && BN == 256 && WGM == 2 && WGN == 4 && !NT;
 
   // One LDS array per stage slot (x image, then the weight tiles and their padding); with
   // STAGE_Y one array of all NST slots, which the epilogue reuses for the block's output tile.
@@ -495,6 +498,77 @@ tiled_gemm_kernel(TiledArgs a) {
       pair(q0 + 1, std::integral_constant<int, 1>{}, 2 * q0 + 2 < nloc, 2 * q0 + 3 < nloc);
     }
     if (!row1) __builtin_amdgcn_s_barrier();
+  } else if constexpr (PW) {
+    // W8A16 ping-pong, one stage per phase: wave row 1 starts one barrier late, then each wave
+    // alternates a memory phase (its DMA share of stage kt + NST - 1, its fragment reads of
+    // stage kt, the dequantization of its first weight tile) and an MFMA phase (64 MFMAs, with
+    // the other three tiles dequantized between the MFMAs of the tiles before them, two VALU ops
+    // after each MFMA), two barriers per stage. Every DMA is issued at the top of a memory phase,
+    // into the slot of stage kt - 1, which both rows finished reading before the barrier that
+    // opened the phase; a wave's wait (all but its newest stage) lands its share of stage
+    // kt + 1 before the barrier that opens row 0's reads of it. Same summation order as the
+    // 1 x 8 layout (each output adds its K stages in order, lo then hi half), so bit-identical.
+    // The dequantization is duplicated over the two rows but runs beside MFMAs of the same wave;
+    // the x fragment reads per stage halve (160 against 272 KB of LDS reads per block).
+    static_assert(NST == 3 && TN == 4 && TM == 8, "W8A16 256 x 256 ping-pong");
+    const bool row1 = wm == 1;
+#pragma unroll
+    for (int i = 0; i < NST - 1; ++i) {
+      load_x(i, i);
+      load_w(i, i);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+    __builtin_amdgcn_s_barrier();
+    if (row1) __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    auto step = [&](int kt, int i, bool live) {
+      load_x(kt + NST - 1, (i + NST - 1) % NST);
+      load_w(kt + NST - 1, (i + NST - 1) % NST);
+      const uint4* xs = xslot(i);
+      const uint4* ws = wslot(i) + 64 * wn * TN + lane;
+      uint4 wraw[TN], x0[TM], x1[TM];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) wraw[j] = ws[64 * j];
+#pragma unroll
+      for (int ii = 0; ii < TM; ++ii) {
+        const int r = wm * WM + 16 * ii + r16;
+        const int sw = tiled_swz<I8>(r);
+        x0[ii] = xs[r * XCH + ((2 * g) ^ sw)];
+        x1[ii] = xs[r * XCH + ((2 * g + 1) ^ sw)];
+      }
+      bf16x8 lo[TN], hi[TN];
+      dequant16(wraw[0], lo[0], hi[0]);
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(63));
+      if (row1) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (live) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if (j + 1 < TN) dequant16(wraw[j + 1], lo[j + 1], hi[j + 1]);
+#pragma unroll
+          for (int ii = 0; ii < TM; ++ii) {
+            acc[ii][j] = mfma16x16x32(lo[j], as_bf16x8(x0[ii]), acc[ii][j]);
+            acc[ii][j] = mfma16x16x32(hi[j], as_bf16x8(x1[ii]), acc[ii][j]);
+          }
+        }
+        // One MFMA, then two VALU ops of the next tile's dequantization. On MI355X the MFMA
+        // phase took 1259-1329 clocks against 1400-1449 with each tile dequantized just before
+        // its MFMAs, the compiler's own order.
+#pragma unroll
+        for (int k = 0; k < 2 * TM * TN; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (!row1) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * LOADS));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    run_steps(step);
+    if (!row1) __builtin_amdgcn_s_barrier();
   } else {
     // Prologue: stages 0 .. NST-2 in flight.
 #pragma unroll
@@ -673,15 +747,17 @@ struct TiledShape {
 template <bool I8, int BM, int BN, bool GLU>
 static const void* tiled_fn() {
   // LDS per block: NST x (x stage + weight stage) <= 160 KB; 128 x 128 tiles keep two blocks
-  // per CU. Wave layout 2 x 4, except the W8A16 tiles 256 wide: there 1 x 8 (BM x 32 per wave)
-  // dequantizes each weight tile in one wave instead of two, on MI355X 2-9 % faster for
-  // 256 x 256 and 9-12 % for 128 x 256 (it reads twice the x fragments, which the conflict-free
-  // swizzle and LDS's 256 bytes per clock of b128 reads absorb). In W8A8 (no dequantization)
-  // 2 x 4 stays faster. Stage slots: 3 for bf16 x (4 would not fit the 256 x 256 tile, and
+  // per CU. Wave layout 2 x 4, except the W8A16 128 x 256 tile: there 1 x 8 (128 x 32 per wave)
+  // dequantizes each weight tile in one wave instead of two, on MI355X 9-12 % faster (it reads
+  // twice the x fragments, which the conflict-free swizzle and LDS's 256 bytes per clock of
+  // b128 reads absorb). The W8A16 256 x 256 tile ran 1 x 8 as well (2-9 % faster than 2 x 4
+  // with the common schedule) until its ping-pong schedule (PW), which on MI355X through the
+  // library is 2-3 % faster at M = 8192 and 0-3 % at 512 and 2048 (alternated, one box). In
+  // W8A8 (no dequantization) 2 x 4 stays faster. Stage slots: 3 for bf16 x (4 would not fit the 256 x 256 tile, and
   // measured no faster on the others), 4 for int8 x (with the 256 x 256 tile's ping-pong schedule
   // 1-2 % faster than 3).
   constexpr int nst = I8 ? 4 : 3;
-  constexpr int wgm = (!I8 && BN == 256) ? 1 : 2;
+  constexpr int wgm = (!I8 && BN == 256 && BM != 256) ? 1 : 2;
   static_assert(64 * wgm * (8 / wgm) == kTiledThreads, "8 waves");
   return reinterpret_cast<const void*>(
       &tiled_gemm_kernel<I8, BM, BN, wgm, 8 / wgm, nst, GLU>);
@@ -746,7 +822,7 @@ static const void* tiled_kernel_for(const TiledShape& sh, bool decode = false,
     if constexpr (!I8 && !GLU) {
       if (stage_y)
         return reinterpret_cast<const void*>(
-            &tiled_gemm_kernel<false, 256, 256, 1, 8, 3, false, false, false, true>);
+            &tiled_gemm_kernel<false, 256, 256, 2, 4, 3, false, false, false, true>);
     } else if constexpr (I8 && !GLU) {
       if (stage_y)
         return reinterpret_cast<const void*>(
