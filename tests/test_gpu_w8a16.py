@@ -453,3 +453,30 @@ def test_staged_output_tiles_bit_identical(pkg, dev, m, n, k):
         golden = (x.double() @ q.double().t()) * s.double()[None, :]
         ok, msg = check_rows_in_chunks(a.contiguous(), golden)
         assert ok, f"M={m} N={n}: {msg}"
+
+
+@pytest.mark.parametrize("k", [64, 80, 1040])
+def test_ping_pong_tile_with_short_and_odd_k(pkg, dev, k):
+    """The W8A16 256 x 256 tile runs two wave rows half a stage apart over groups of three stage
+    slots: one K step (64), two with a 16-wide tail (80) and 17 steps (1040) leave the last group
+    partly empty. On 256 CUs 3000 x 20000 runs that tile over its first 16384 rows (768 blocks in
+    three rounds, the last block row 184 tokens) and 256 x 192 tiles over the rest; staged output
+    with a 16-byte aligned row stride, direct stores without: the same bits, within the tolerance
+    of the fp64 product on the GPU, and row for row the bits of the first 1100 rows run alone
+    (128 x 256 tiles, same summation order)."""
+    m, n = 3000, 20000
+    gen = torch.Generator(device="cpu").manual_seed(6100 + k)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dev)
+    q, s = pkg.ops.quantize_weight_per_channel(w)
+    del w
+    qp = pkg.ops.pack_weight(q)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+    a = _abi_prefill(pkg, dev, x, qp, s, n, n)
+    b = _abi_prefill(pkg, dev, x, qp, s, n, n + 4)
+    assert torch.equal(a.contiguous().view(torch.int16), b.contiguous().view(torch.int16)), f"K={k}"
+    golden = (x.double() @ q.double().t()) * s.double()[None, :]
+    ok, msg = check_rows_in_chunks(a.contiguous(), golden)
+    assert ok, f"K={k}: {msg}"
+    del golden
+    y_small = pkg.ops.w8a16_linear(x[:1100], qp, s, algo=PREFILL)
+    assert torch.equal(a[:1100].contiguous().view(torch.int16), y_small.view(torch.int16)), f"K={k}"
