@@ -25,10 +25,14 @@
 //  * x rows are stored 16-byte-chunk swizzled (chunk c of row r at c ^ swz(r)) so the fragment
 //    reads of 16 rows at one K offset have no LDS bank conflicts (tiled_swz).
 //  * One barrier per stage: after it, the stage's loads from every wave have landed and every
-//    wave has finished reading the slot the next loads overwrite.
+//    wave has finished reading the slot the next loads overwrite. The 256 x 256 tiles instead
+//    run their two wave rows half a phase apart, two barriers per phase, so one wave's MFMAs run
+//    while the other wave of its SIMD reads (ping-pong: PING in W8A8, pairs of stages per phase;
+//    PW in W8A16, one stage per phase).
 //  * Output: each lane stores its four bf16 of a 16 x 16 tile directly (8 bytes), except in
-//    W8A16 256 x 256 launches of three or more rounds of blocks, where the block's tile is staged
-//    in the stage ring once the K loop is done and written as whole rows (STAGE_Y).
+//    256 x 256 launches of three or more rounds of blocks (W8A16) or more than one round without
+//    an int32 output (W8A8), where the tile is staged in the stage ring once the K loop is done
+//    and written as whole rows (STAGE_Y).
 //
 // Tile order. Blocks are dispatched round-robin over the 8 XCDs; the tile index is remapped so
 // each XCD runs a contiguous range of tiles, in groups of kGroupM token blocks x consecutive
