@@ -78,6 +78,7 @@ struct SkinnyArgs {
   int NSU;              // super-steps per unit: ceil(ssteps / W) rounded up to a multiple of DW
   void* part;           // S > 1: raw partial sums [S][M][16 nrb], fp32 (W8A16) or int32 (W8A8)
   int glu;              // gate/up layout: I, the output columns (N = 16 nrb packed rows); else 0
+  int pairs;            // > 0: workgroups i and i + pairs share a CU and split its units
 };
 
 // Register stage of the weight ring: one 1 KB tile per row tile of the panel.
@@ -107,7 +108,7 @@ __host__ __device__ constexpr int skinny_swz_mask(int chunks_per_row) {
 }
 
 template <bool I8, int MT, int RT, int W, int DW, int DX, bool XLDS, bool GLU, bool BFW = false,
-          bool QX = false>
+          bool QX = false, bool PAIR = false>
 __global__ void __launch_bounds__(64 * W)
 skinny_kernel(SkinnyArgs a) {
   using Acc = std::conditional_t<I8, i32x4, f32x4>;
@@ -165,8 +166,17 @@ skinny_kernel(SkinnyArgs a) {
   const int r16 = lane & 15;
   const int g = lane >> 4;
   const int G = gridDim.x;
-  const int u_first = blockIdx.x * a.units / G;
-  const int u_end = (blockIdx.x + 1) * a.units / G;
+  // Units [u_first, u_end) of this workgroup: an even spread of whole units over the grid, or
+  // (PAIR, a grid of exactly 2 a.pairs workgroups, two resident per CU) one over a.pairs CU slots:
+  // the dispatcher gives every CU its first workgroup before any CU its second, so workgroups i
+  // and i + a.pairs share a CU and split that CU's units, the first taking the larger half.
+  const bool second = PAIR && (int)blockIdx.x >= a.pairs;
+  const unsigned slot = second ? blockIdx.x - (unsigned)a.pairs : blockIdx.x;
+  const unsigned nslots = PAIR ? (unsigned)a.pairs : (unsigned)G;
+  const int s0 = slot * a.units / nslots, s1 = (slot + 1) * a.units / nslots;
+  const int smid = s0 + ((s1 - s0 + 1) >> 1);
+  const int u_first = second ? smid : s0;
+  const int u_end = PAIR && !second ? smid : s1;
   const bool split = a.splits > 1;
 
   const BufferRsrc qres =
@@ -636,6 +646,13 @@ static const void* skinny_fn() {
   return reinterpret_cast<const void*>(&skinny_kernel<I8, MT, RT, W, DW, DX, XLDS, GLU, BFW, QX>);
 }
 
+// The paired-grid form of the M <= 16 kernel with staged activations (skinny_plan_for).
+template <bool I8>
+static const void* skinny_paired_fn() {
+  return reinterpret_cast<const void*>(
+      &skinny_kernel<I8, 1, 1, 8, 4, 1, true, false, false, false, true>);
+}
+
 // Panel height for 17..64 tokens: each panel re-reads the activations from L2, so panels are as
 // tall as the row-tile count allows while still giving every CU work (measured on MI355X: 64-row
 // panels from 1024 row tiles up, 32-row panels from 384).
@@ -722,6 +739,16 @@ struct SkinnyPlan {
   int64_t part_bytes;  // workspace for the raw partial sums (0 when S = 1)
 };
 
+static int skinny_device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return cus;
+}
+
 // Whole units per workgroup, spread as evenly as whole units allow over the resident
 // workgroups; with S = 1 the scales of a workgroup's panels must fit its LDS array.
 static int skinny_grid(int units, int rt, bool split, int resident) {
@@ -733,7 +760,7 @@ static int skinny_grid(int units, int rt, bool split, int resident) {
 // The plan of one call for a given configuration: kernel, unit counts, grid and workspace size.
 template <bool I8>
 static SkinnyPlan skinny_plan_for(const SkinnyShape& sh, const void* fn, int64_t M, int64_t N,
-                                  int64_t K) {
+                                  int64_t K, const void* paired_fn = nullptr) {
   SkinnyPlan pl;
   pl.sh = sh;
   pl.fn = fn;
@@ -750,7 +777,20 @@ static SkinnyPlan skinny_plan_for(const SkinnyShape& sh, const void* fn, int64_t
   a.ssteps = (int)ceil_div(a.nsteps, sh.splits);
   a.units = a.panels * sh.splits;
   a.NSU = (int)(ceil_div(ceil_div(a.ssteps, sh.w), sh.dw) * sh.dw);
-  pl.grid = skinny_grid(a.units, sh.rt, sh.splits > 1, persistent_blocks(fn, 64 * sh.w, pl.x_lds));
+  const int resident = persistent_blocks(fn, 64 * sh.w, pl.x_lds);
+  pl.grid = skinny_grid(a.units, sh.rt, sh.splits > 1, resident);
+  // With two workgroups resident per CU and at least two units per CU, whole units spread over
+  // the workgroups leave some CUs a unit more than others (gate_up at M <= 16: 1792 units as 448
+  // workgroups of 4, so 192 CUs stream 8 units and 64 stream 4, against 7 each); a paired grid
+  // gives every CU the same share, split 4 + 3 between its two workgroups.
+  const int cus = paired_fn && resident > 0 ? skinny_device_cus() : 0;
+  if (sh.splits == 1 && cus > 0 && resident >= 2 * cus && a.units >= 2 * cus &&
+      ceil_div(ceil_div(a.units, cus), 2) <= kSkinnyScaleLds / (16 * sh.rt) &&
+      ceil_div(a.units, pl.grid) * ceil_div(pl.grid, cus) > ceil_div(a.units, cus)) {
+    a.pairs = cus;
+    pl.grid = 2 * cus;
+    pl.fn = paired_fn;  // the same kernel's paired form: same resources, so the same residency
+  }
   pl.part_bytes = sh.splits > 1 ? (int64_t)sh.splits * M * 16 * a.nrb * 4 : 0;
   return pl;
 }
@@ -764,7 +804,9 @@ static SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t glu = 0,
   const void* fn = glu > 0 ? skinny_kernel_for<I8, true>(sh)
                    : bfw   ? skinny_kernel_for<false, false, true>(sh)
                            : skinny_kernel_for<I8>(sh);
-  SkinnyPlan pl = skinny_plan_for<I8>(sh, fn, M, N, K);
+  const bool pairable = glu == 0 && !bfw && sh.mt == 1 && sh.xlds && sh.dw == 4;
+  SkinnyPlan pl =
+      skinny_plan_for<I8>(sh, fn, M, N, K, pairable ? skinny_paired_fn<I8>() : nullptr);
   pl.a.glu = (int)glu;
   return pl;
 }
