@@ -9,8 +9,9 @@
 // Work decomposition.
 //  * A panel is RT row tiles (16 * RT weight rows). The K steps split into S ranges of `ssteps`
 //    steps; a work unit is (split, panel), numbered split-major. Each workgroup takes a
-//    contiguous range of whole units (split as evenly as whole units allow) and streams them one
-//    after another.
+//    contiguous range of whole units (split as evenly as whole units allow, or, on a paired grid,
+//    each CU's share split between the two workgroups it holds) and streams them one after
+//    another.
 //  * Within a unit the W waves split the unit's 64-wide K steps round-robin (wave w takes steps
 //    w, w + W, ...; a "super-step" is one step of every wave). A wave multiplies each activation
 //    fragment against all RT row tiles of the panel, so activations are read 2M/(16 RT) times
